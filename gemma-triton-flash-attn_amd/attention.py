@@ -1,0 +1,208 @@
+"""Host orchestration of the gfx950 GQA flash-attention path (the reference's public API).
+
+Mirrors /root/reference/flash_attn/attention.py:
+  * ``attention_flash_gqa``   inference forward, no LSE (reference 540-604)
+  * ``FlashAttnGQAFunction``  autograd function: forward stores LSE, backward runs the
+                              dQ kernel (fused delta) then the pack-GQA dKV kernel (1433-1622)
+  * ``flash_attn_gqa_train``  training entry point (1625-1635)
+  * ``attention``             plain (non-causal, MHA) scaled dot-product attention (11-17)
+
+Tensors are (B, H, N, D) with any (batch, head, row) strides and a unit-stride head dim;
+query head h uses KV head h // (Hq // Hkv). ``slide_size`` > 0 with ``causal`` limits query
+i to keys in [i - slide_size + 1, i]; a window is ignored when not causal and a window
+covering the whole sequence is plain causal (reference 1441-1443).
+
+Every call goes through libgfa.so's C ABI on the caller's current HIP stream. There is no
+CPU or PyTorch fallback: unsupported inputs raise before anything is launched.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from .registry import lookup
+
+_DTYPES = {torch.float16: _lib.GFA_DTYPE_FP16, torch.bfloat16: _lib.GFA_DTYPE_BF16}
+
+
+def _needs_copy(t: torch.Tensor) -> bool:
+    s = t.stride()
+    return (s[3] != 1 or any(x % 8 for x in s[:3]) or any(x < 0 for x in s[:3]) or t.data_ptr() % 16 != 0)
+
+
+def _prep(t: torch.Tensor) -> torch.Tensor:
+    """Rows must be 16-byte aligned with a unit-stride head dim; copy otherwise."""
+    return t.contiguous() if _needs_copy(t) else t
+
+
+def _check_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 4-D (B, H, N, D)")
+    B, Hq, N, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[2] != N or k.shape[3] != D:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    Hkv = k.shape[1]
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"N_Q_HEADS={Hq} must be a multiple of N_KV_HEADS={Hkv}")
+    if q.dtype not in _DTYPES:
+        raise TypeError(f"dtype {q.dtype} not supported (fp16 / bf16)")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k, v must share one dtype")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("q, k, v must be GPU tensors (the engine has no CPU path)")
+    if k.device != q.device or v.device != q.device:
+        raise ValueError("q, k, v must be on the same device")
+    lookup(D)
+    if N == 0 or B == 0:
+        raise ValueError("empty sequence or batch")
+
+
+def _norm_window(causal: bool, slide_size: int, n: int) -> int:
+    """attention.py:1441-1443: a window covering the whole sequence is plain causal.
+    The library ignores the window when not causal (reference kernel 289-293)."""
+    if slide_size is None:
+        slide_size = 0
+    slide_size = int(slide_size)
+    if slide_size < 0:
+        raise ValueError("slide_size must be >= 0")
+    if slide_size > 0 and slide_size >= n:
+        slide_size = 0
+    return slide_size
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bool, block_kv: int = 0):
+    B, Hq, N, D = q.shape
+    Hkv = k.shape[1]
+    q, k, v = _prep(q), _prep(k), _prep(v)
+    o = torch.empty_like(q)
+    if _needs_copy(o):
+        o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device) if store_lse else None
+    a = _lib.FwdArgs()
+    a.q, a.k, a.v, a.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    a.lse = lse.data_ptr() if lse is not None else None
+    a.q_strides, a.k_strides, a.v_strides, a.o_strides = (_lib.strides_of(t) for t in (q, k, v, o))
+    a.batch, a.heads_q, a.heads_kv, a.seq_len, a.head_dim = B, Hq, Hkv, N, D
+    a.causal = int(bool(causal))
+    a.window = int(slide_size)
+    a.scale = float(scale)
+    a.dtype = _DTYPES[q.dtype]
+    a.block_kv = int(block_kv)
+    a.stream = _stream(q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(_lib.load().gfa_fwd(ctypes.byref(a)))
+    return o, lse
+
+
+def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, q_splits: int = 0):
+    B, Hq, N, D = q.shape
+    Hkv = k.shape[1]
+    do = _prep(do)
+    if do.dtype != q.dtype:
+        do = do.to(q.dtype)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dq, dk, dv = (t if not _needs_copy(t) else torch.empty(t.shape, dtype=t.dtype, device=t.device)
+                  for t in (dq, dk, dv))
+    delta = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device)
+    lib = _lib.load()
+    ws_bytes = int(lib.gfa_bwd_workspace_size(B, Hq, Hkv, N, D, int(bool(causal)), int(slide_size), int(q_splits)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    a = _lib.BwdArgs()
+    a.q, a.k, a.v, a.o, a.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr()
+    a.lse, a.delta = lse.data_ptr(), delta.data_ptr()
+    a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    (a.q_strides, a.k_strides, a.v_strides, a.o_strides, a.do_strides, a.dq_strides, a.dk_strides,
+     a.dv_strides) = (_lib.strides_of(t) for t in (q, k, v, o, do, dq, dk, dv))
+    a.batch, a.heads_q, a.heads_kv, a.seq_len, a.head_dim = B, Hq, Hkv, N, D
+    a.causal = int(bool(causal))
+    a.window = int(slide_size)
+    a.scale = float(scale)
+    a.dtype = _DTYPES[q.dtype]
+    a.q_splits = int(q_splits)
+    a.workspace = ws.data_ptr() if ws is not None else None
+    a.workspace_bytes = ws_bytes
+    a.stream = _stream(q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.gfa_bwd(ctypes.byref(a)))
+    return dq, dk, dv, delta
+
+
+def _default_scale(d: int, scale: float | None) -> float:
+    return 1.0 / math.sqrt(d) if scale is None else float(scale)
+
+
+class FlashAttnGQAFunction(torch.autograd.Function):
+    """Autograd function of the GQA flash attention (reference attention.py:1433-1622).
+
+    forward(q, k, v, causal, slide_size, scale=None) -> O; saves q, k, v, O and the fp32 LSE.
+    backward(dO) -> dQ, dK, dV via gfa_bwd (dQ kernel with fused delta, then pack-GQA dKV).
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal=False, slide_size=0, scale=None):
+        _check_inputs(q, k, v)
+        slide_size = _norm_window(causal, slide_size, q.shape[2])
+        sc = _default_scale(q.shape[3], scale)
+        o, lse = _forward(q, k, v, causal, slide_size, sc, store_lse=True)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.causal = bool(causal)
+        ctx.slide_size = slide_size
+        ctx.scale = sc
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        q, k, v = _prep(q), _prep(k), _prep(v)
+        dq, dk, dv, _ = _backward(q, k, v, o, lse, do, ctx.causal, ctx.slide_size, ctx.scale)
+        return dq, dk, dv, None, None, None
+
+
+def flash_attn_gqa_train(q, k, v, causal=False, slide_size=0, *, scale=None):
+    """Flash attention with autograd support (reference attention.py:1625-1635).
+
+    q: (B, N_Q_HEADS, N, D); k, v: (B, N_KV_HEADS, N, D); fp16 or bf16; D in {256, 512}.
+    ``scale`` defaults to 1/sqrt(D) like the reference; other values are used natively.
+    """
+    return FlashAttnGQAFunction.apply(q, k, v, causal, slide_size, scale)
+
+
+def attention_flash_gqa(q, k, v, causal=False, slide_size=0, BLOCK_Q=None, BLOCK_KV=None, BLOCK_D=None,
+                        num_warps=None, num_stages=None, *, scale=None):
+    """Inference forward without LSE (reference attention.py:540-604). Default causal=False.
+
+    ``BLOCK_KV`` selects one of the built LDS tile widths for this head dim. ``BLOCK_Q``,
+    ``BLOCK_D``, ``num_warps`` and ``num_stages`` are Triton launch knobs of the reference;
+    they are accepted for call compatibility and have no effect here (the gfx950 kernels
+    always run 32-row wave pairs with the registry's tiles).
+    """
+    _check_inputs(q, k, v)
+    D = q.shape[3]
+    cfg = lookup(D)
+    bkv = 0
+    if BLOCK_KV is not None:
+        if int(BLOCK_KV) not in cfg.fwd_block_kv_options:
+            raise ValueError(f"BLOCK_KV={BLOCK_KV} not built for head_dim={D}; options {cfg.fwd_block_kv_options}")
+        bkv = int(BLOCK_KV)
+    if BLOCK_D is not None and int(BLOCK_D) != D:
+        raise ValueError("BLOCK_D must equal HEAD_DIM (no head-dim tiling)")
+    slide_size = _norm_window(causal, slide_size, q.shape[2])
+    o, _ = _forward(q, k, v, causal, slide_size, _default_scale(D, scale), store_lse=False, block_kv=bkv)
+    return o
+
+
+def attention(q, k, v):
+    """Standard (non-causal, MHA) scaled dot-product attention (reference attention.py:11-17),
+    computed by the same HIP forward kernel."""
+    if q.shape[1] != k.shape[1]:
+        raise ValueError("attention() is the MHA form; use attention_flash_gqa for GQA")
+    return attention_flash_gqa(q, k, v, causal=False)

@@ -1,0 +1,290 @@
+// C ABI of the engine: argument validation, the HEAD_DIM-keyed tile registry, work
+// decomposition and kernel dispatch. Nothing here allocates, frees or synchronises.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/gfa.h"
+#include "gfa_launch.h"
+#include "gfa_params.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return GFA_OK;
+}
+
+// ---------------------------------------------------------------------------------
+// HEAD_DIM-keyed registry (mirrors registry.py). Replaces the reference's if/else tile
+// tables (/root/reference/flash_attn/attention.py:561-579, 1445-1451, 1498-1504,
+// 1536-1564) with MI355X tiles: every kernel works on wave pairs that split the head
+// dim, 32 rows per pair, NW waves per workgroup.
+// ---------------------------------------------------------------------------------
+struct Entry {
+  int head_dim;
+  int fwd_bkv, fwd_waves;
+  int dq_bkv, dq_waves;
+  int dkv_bq, dkv_waves;
+};
+
+constexpr Entry kRegistry[] = {
+    {512, 32, 4, 32, 4, 32, 4},
+    {256, 64, 4, 32, 4, 32, 4},
+};
+
+const Entry* lookup(int d) {
+  for (const Entry& e : kRegistry)
+    if (e.head_dim == d) return &e;
+  return nullptr;
+}
+
+bool fwd_built(int d, int bkv, int nw) {
+  return (d == 512 && bkv == 32 && (nw == 4 || nw == 8)) || (d == 256 && (bkv == 32 || bkv == 64) && nw == 4);
+}
+
+int largest_pow2_divisor_le(int r, int cap) {
+  int x = 1;
+  while (x * 2 <= cap && r % (x * 2) == 0) x *= 2;
+  return x;
+}
+
+gfa::QGrid make_qgrid(int B, int Hkv, int R, int N, int nw) {
+  gfa::QGrid g;
+  const int nu = nw / 2;
+  g.hpw = largest_pow2_divisor_le(R, nu);
+  g.qbw = nu / g.hpw;
+  g.n_hg = R / g.hpw;
+  g.n_qsb = (N + 32 * g.qbw - 1) / (32 * g.qbw);
+  g.nblocks = g.n_qsb * B * Hkv * g.n_hg;
+  return g;
+}
+
+// Smallest of {1, 2, 4, 8} giving at least one workgroup per CU (256 CUs on MI355X).
+int pick_q_splits(int B, int Hkv, int N, int nw) {
+  const int keys_per_wg = 32 * (nw / 2);
+  const int grid = ((N + keys_per_wg - 1) / keys_per_wg) * B * Hkv;
+  int qs = 1;
+  while (qs < 8 && grid * qs < 256) qs *= 2;
+  return qs;
+}
+
+gfa::RowView rv(const gfa_strides& s) { return gfa::RowView{s.batch, s.head, s.row}; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_view(const char* name, const void* ptr, const gfa_strides& s, bool need_ptr) {
+  if (need_ptr && ptr == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+  if (ptr != nullptr && !aligned16(ptr)) return fail(GFA_ERR_INVALID_ARGUMENT, "%s is not 16-byte aligned", name);
+  if ((s.row & 7) != 0 || (s.head & 7) != 0 || (s.batch & 7) != 0)
+    return fail(GFA_ERR_INVALID_ARGUMENT, "%s strides (%lld, %lld, %lld) must be multiples of 8 elements", name,
+                (long long)s.batch, (long long)s.head, (long long)s.row);
+  if (s.row < 0 || s.head < 0 || s.batch < 0) return fail(GFA_ERR_INVALID_ARGUMENT, "%s has negative strides", name);
+  return GFA_OK;
+}
+
+int check_dims(int B, int Hq, int Hkv, int N, int D, int dtype, int window) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || N <= 0)
+    return fail(GFA_ERR_INVALID_ARGUMENT, "empty problem: B=%d Hq=%d Hkv=%d N=%d", B, Hq, Hkv, N);
+  if (Hq % Hkv != 0) return fail(GFA_ERR_INVALID_ARGUMENT, "heads_q=%d is not a multiple of heads_kv=%d", Hq, Hkv);
+  if (lookup(D) == nullptr) return fail(GFA_ERR_UNSUPPORTED, "head_dim=%d is not in the registry (256, 512)", D);
+  if (dtype != GFA_DTYPE_FP16 && dtype != GFA_DTYPE_BF16) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+  if (window < 0) return fail(GFA_ERR_INVALID_ARGUMENT, "window=%d must be >= 0", window);
+  return GFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gfa_last_error(void) { return g_err; }
+
+int gfa_version(void) { return GFA_VERSION; }
+
+int gfa_config(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len, int32_t head_dim,
+               gfa_config_info* out) {
+  if (out == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "out is NULL");
+  const Entry* e = lookup(head_dim);
+  if (e == nullptr) return fail(GFA_ERR_UNSUPPORTED, "head_dim=%d is not in the registry (256, 512)", head_dim);
+  if (heads_kv <= 0 || heads_q % heads_kv != 0 || batch <= 0 || seq_len <= 0)
+    return fail(GFA_ERR_INVALID_ARGUMENT, "bad problem size");
+  const gfa::QGrid g = make_qgrid(batch, heads_kv, heads_q / heads_kv, seq_len, e->fwd_waves);
+  out->head_dim = head_dim;
+  out->fwd_block_q = 32 * g.qbw;
+  out->fwd_block_kv = e->fwd_bkv;
+  out->fwd_waves = e->fwd_waves;
+  const gfa::QGrid gq = make_qgrid(batch, heads_kv, heads_q / heads_kv, seq_len, e->dq_waves);
+  out->dq_block_q = 32 * gq.qbw;
+  out->dq_block_kv = e->dq_bkv;
+  out->dq_waves = e->dq_waves;
+  out->dkv_block_kv = 32 * (e->dkv_waves / 2);
+  out->dkv_block_q = e->dkv_bq;
+  out->dkv_waves = e->dkv_waves;
+  out->q_splits = pick_q_splits(batch, heads_kv, seq_len, e->dkv_waves);
+  return ok();
+}
+
+int gfa_fwd(const gfa_fwd_args* a) {
+  if (a == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "args is NULL");
+  int rc = check_dims(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->dtype, a->window);
+  if (rc) return rc;
+  if ((rc = check_view("q", a->q, a->q_strides, true))) return rc;
+  if ((rc = check_view("k", a->k, a->k_strides, true))) return rc;
+  if ((rc = check_view("v", a->v, a->v_strides, true))) return rc;
+  if ((rc = check_view("o", a->o, a->o_strides, true))) return rc;
+  if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
+  const Entry* e = lookup(a->head_dim);
+  const int bkv = a->block_kv ? a->block_kv : e->fwd_bkv;
+  const int nw = e->fwd_waves;
+  if (!fwd_built(a->head_dim, bkv, nw))
+    return fail(GFA_ERR_UNSUPPORTED, "no forward kernel built for head_dim=%d block_kv=%d", a->head_dim, bkv);
+
+  gfa::FwdParams p;
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<uint16_t*>(a->o);
+  p.lse = a->lse;
+  p.qv = rv(a->q_strides);
+  p.kv = rv(a->k_strides);
+  p.vv = rv(a->v_strides);
+  p.ov = rv(a->o_strides);
+  p.B = a->batch;
+  p.Hq = a->heads_q;
+  p.Hkv = a->heads_kv;
+  p.N = a->seq_len;
+  p.R = a->heads_q / a->heads_kv;
+  p.causal = a->causal ? 1 : 0;
+  // attention.py:1441-1443: a window covering the whole sequence is plain causal.
+  p.window = (a->causal && a->window > 0 && a->window < a->seq_len) ? a->window : 0;
+  p.scale_log2 = a->scale * 1.4426950408889634f;
+  p.store_lse = a->lse != nullptr;
+  p.g = make_qgrid(p.B, p.Hkv, p.R, p.N, nw);
+  if (p.g.nblocks <= 0) return fail(GFA_ERR_INVALID_ARGUMENT, "empty grid");
+  const hipError_t err = gfa::launch_fwd(p, a->head_dim, bkv, nw, a->dtype == GFA_DTYPE_BF16,
+                                         static_cast<hipStream_t>(a->stream));
+  if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "forward launch failed: %s", hipGetErrorString(err));
+  return ok();
+}
+
+size_t gfa_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len, int32_t head_dim,
+                              int32_t causal, int32_t window, int32_t q_splits) {
+  (void)heads_q;
+  (void)causal;
+  (void)window;
+  const Entry* e = lookup(head_dim);
+  if (e == nullptr || batch <= 0 || heads_kv <= 0 || seq_len <= 0) return 0;
+  const int qs = q_splits > 0 ? q_splits : pick_q_splits(batch, heads_kv, seq_len, e->dkv_waves);
+  if (qs <= 1) return 0;
+  return (size_t)qs * 2 * batch * heads_kv * (size_t)seq_len * head_dim * sizeof(float);
+}
+
+int gfa_bwd(const gfa_bwd_args* a) {
+  if (a == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "args is NULL");
+  int rc = check_dims(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->dtype, a->window);
+  if (rc) return rc;
+  if ((rc = check_view("q", a->q, a->q_strides, true))) return rc;
+  if ((rc = check_view("k", a->k, a->k_strides, true))) return rc;
+  if ((rc = check_view("v", a->v, a->v_strides, true))) return rc;
+  if ((rc = check_view("o", a->o, a->o_strides, true))) return rc;
+  if ((rc = check_view("dout", a->dout, a->do_strides, true))) return rc;
+  if ((rc = check_view("dq", a->dq, a->dq_strides, true))) return rc;
+  if ((rc = check_view("dk", a->dk, a->dk_strides, true))) return rc;
+  if ((rc = check_view("dv", a->dv, a->dv_strides, true))) return rc;
+  if (a->lse == nullptr || a->delta == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "lse and delta are required");
+  if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
+  const Entry* e = lookup(a->head_dim);
+  const int qs = a->q_splits > 0 ? a->q_splits : pick_q_splits(a->batch, a->heads_kv, a->seq_len, e->dkv_waves);
+  if (qs != 1 && qs != 2 && qs != 4 && qs != 8) return fail(GFA_ERR_INVALID_ARGUMENT, "q_splits=%d not in {1,2,4,8}", qs);
+  const size_t need = gfa_bwd_workspace_size(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->causal,
+                                             a->window, qs);
+  if (need > 0 && (a->workspace == nullptr || a->workspace_bytes < need))
+    return fail(GFA_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, a->workspace_bytes);
+  if (need > 0 && !aligned16(a->workspace)) return fail(GFA_ERR_INVALID_ARGUMENT, "workspace is not 16-byte aligned");
+
+  const bool bf16 = a->dtype == GFA_DTYPE_BF16;
+  const int R = a->heads_q / a->heads_kv;
+  const int window = (a->causal && a->window > 0 && a->window < a->seq_len) ? a->window : 0;
+  const float scale_log2 = a->scale * 1.4426950408889634f;
+  hipStream_t stream = static_cast<hipStream_t>(a->stream);
+
+  gfa::BwdDqParams pq;
+  pq.q = static_cast<const uint16_t*>(a->q);
+  pq.k = static_cast<const uint16_t*>(a->k);
+  pq.v = static_cast<const uint16_t*>(a->v);
+  pq.o = static_cast<const uint16_t*>(a->o);
+  pq.dout = static_cast<const uint16_t*>(a->dout);
+  pq.lse = a->lse;
+  pq.delta = a->delta;
+  pq.dq = static_cast<uint16_t*>(a->dq);
+  pq.qv = rv(a->q_strides);
+  pq.kv = rv(a->k_strides);
+  pq.vv = rv(a->v_strides);
+  pq.ov = rv(a->o_strides);
+  pq.dov = rv(a->do_strides);
+  pq.dqv = rv(a->dq_strides);
+  pq.B = a->batch;
+  pq.Hq = a->heads_q;
+  pq.Hkv = a->heads_kv;
+  pq.N = a->seq_len;
+  pq.R = R;
+  pq.causal = a->causal ? 1 : 0;
+  pq.window = window;
+  pq.scale = a->scale;
+  pq.scale_log2 = scale_log2;
+  pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves);
+  hipError_t err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, bf16, stream);
+  if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dQ launch failed: %s", hipGetErrorString(err));
+
+  gfa::BwdDkvParams pk;
+  pk.q = pq.q;
+  pk.k = pq.k;
+  pk.v = pq.v;
+  pk.dout = pq.dout;
+  pk.lse = a->lse;
+  pk.delta = a->delta;
+  pk.dk = static_cast<uint16_t*>(a->dk);
+  pk.dv = static_cast<uint16_t*>(a->dv);
+  pk.part = static_cast<float*>(a->workspace);
+  pk.qv = pq.qv;
+  pk.kv = pq.kv;
+  pk.vv = pq.vv;
+  pk.dov = pq.dov;
+  pk.dkv = rv(a->dk_strides);
+  pk.dvv = rv(a->dv_strides);
+  pk.B = a->batch;
+  pk.Hq = a->heads_q;
+  pk.Hkv = a->heads_kv;
+  pk.N = a->seq_len;
+  pk.R = R;
+  pk.causal = pq.causal;
+  pk.window = window;
+  pk.scale = a->scale;
+  pk.scale_log2 = scale_log2;
+  pk.q_splits = qs;
+  const int keys_per_wg = 32 * (e->dkv_waves / 2);
+  pk.n_kb = (pk.N + keys_per_wg - 1) / keys_per_wg;
+  pk.nblocks = pk.n_kb * pk.B * pk.Hkv * qs;
+  err = gfa::launch_bwd_dkv(pk, a->head_dim, e->dkv_bq, bf16, stream);
+  if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV launch failed: %s", hipGetErrorString(err));
+  if (qs > 1) {
+    err = gfa::launch_dkv_reduce(pk, a->head_dim, bf16, stream);
+    if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV reduce launch failed: %s", hipGetErrorString(err));
+  }
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,355 @@
+// GQA flash-attention backward, pack-GQA Q-split dK/dV kernel (hot-path row R3) and the
+// fp32 partial-sum reduction used when the query range is split.
+//
+// Semantics follow /root/reference/flash_attn/attention.py:1080-1213 (launch 1602-1620):
+// for a block of keys j of KV head g,
+//   dV_j = sum_{h in group g} sum_i P_ij dO_i
+//   dK_j = s * sum_{h in group g} sum_i dS_ij q_i
+// with P and dS recomputed from LSE and delta exactly as in the dQ kernel, P and dS cast
+// to the input dtype before the products. The query range of a key block starts at the
+// key block (causal) and ends at the last key + window - 1 (sliding window).
+// With q_splits > 1 the (head, query tile) iteration space of every key block is cut into
+// q_splits contiguous chunks; each chunk writes an fp32 partial (scaled) and
+// dkv_reduce_kernel sums them in a fixed order (deterministic, no atomics; the reference
+// uses atomic_add into 16-bit dK/dV, attention.py:1206-1209).
+//
+// MI355X design: wave pairs again. A pair owns 32 keys; each wave keeps its head-dim half
+// of K and V in VGPRs (B operands of S = Q K^T and dP = dO V^T, lane = key) and its half of
+// the dK^T / dV^T accumulators. Per LDS tile of BQ queries the wave computes partial S and
+// dP, swaps them with its partner, forms P and dS on the key lanes (LSE / delta are
+// per-register row values read from global memory), then
+//   dV^T[half] += dO^T[half] P   and   dK^T[half] += Q^T[half] dS,
+// reading the A operands with ds_read_b64_tr_b16 from the row-major dO and Q tiles that
+// fed the score products. All R query heads of the KV head stream through the same
+// workgroup (pack-GQA), so K/V are read once and dK/dV need no cross-head reduction.
+#include "gfa_common.h"
+#include "gfa_params.h"
+#include "gfa_launch.h"
+
+namespace gfa {
+
+template <int D, int BQ, bool IS_BF16, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams p) {
+  constexpr int DH = D / 2;
+  constexpr int KTH = DH / 16;
+  constexpr int DBH = DH / 32;
+  constexpr int SB = BQ / 32;  // 32-query score blocks per tile
+  constexpr int TILE = BQ * D * 2;
+  constexpr int XHALF = SB * 16 * 64 * 4;
+  constexpr int XCH = 2 * XHALF;
+  constexpr int NU = NW / 2;
+  static_assert(BQ % 32 == 0, "BQ must be a multiple of 32");
+  static_assert(DH % 128 == 0, "head dim must be 256 or 512");
+
+  __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NW * XCH];
+  char GFA_LDS* smem = (char GFA_LDS*)smem_raw;
+  char GFA_LDS* xch = smem + 4 * TILE;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int unit = wave >> 1;
+  const int dh = wave & 1;
+  const int h = lane >> 5;
+  const int l32 = lane & 31;
+
+  // ---- workgroup -> (split, b, kv head, key block); early key blocks (most work) first ----
+  int lid = xcd_remap(blockIdx.x, p.nblocks, 4);
+  const int kb = lid % p.n_kb;
+  lid /= p.n_kb;
+  const int kvh = lid % p.Hkv;
+  lid /= p.Hkv;
+  const int b = lid % p.B;
+  const int split = lid / p.B;
+
+  const int wg_k0 = kb * NU * 32;
+  const int wg_k_last = min(p.N, wg_k0 + NU * 32) - 1;
+  const int k0 = wg_k0 + unit * 32;  // this pair's keys [k0, k0 + 32)
+  const bool active = k0 < p.N;
+  const int k_last = k0 + 31;
+  const int key = k0 + l32;
+  const int krow = min(key, p.N - 1);
+
+  const bool swa = p.causal && p.window > 0;
+  // Query tiles the workgroup visits.
+  int qt_lo = 0, qt_hi = (p.N + BQ - 1) / BQ;
+  if (p.causal) {
+    qt_lo = wg_k0 / BQ;
+    if (swa) qt_hi = min(qt_hi, (wg_k_last + p.window - 1) / BQ + 1);
+  }
+  const int nqt = max(0, qt_hi - qt_lo);
+  const int total = p.R * nqt;
+  const int chunk = (total + p.q_splits - 1) / p.q_splits;
+  const int it_lo = min(total, split * chunk);
+  const int it_hi = min(total, it_lo + chunk);
+
+  // Queries any key of this pair serves [vis_lo, vis_hi); queries every key serves [all_lo, all_hi).
+  int vis_lo = 0, vis_hi = p.N, all_lo = 0, all_hi = p.N;
+  if (p.causal) {
+    vis_lo = k0;
+    all_lo = k_last;
+    if (swa) {
+      vis_hi = min(p.N, k_last + p.window);   // q - key < window
+      all_hi = min(p.N, k0 + p.window);
+    }
+  }
+  const bool pair_full = k_last < p.N;
+
+  // ---- K and V halves (B operands: lane = key), resident ----
+  i16x8 kf[KTH], vf[KTH];
+  {
+    const uint16_t* kr = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh + (int64_t)krow * p.kv.sn + dh * DH + 8 * h;
+    const uint16_t* vr = p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh + (int64_t)krow * p.vv.sn + dh * DH + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < KTH; ++kk) {
+      kf[kk] = *reinterpret_cast<const i16x8*>(kr + 16 * kk);
+      vf[kk] = *reinterpret_cast<const i16x8*>(vr + 16 * kk);
+    }
+  }
+
+  f32x16 dk[DBH], dv[DBH];
+#pragma unroll
+  for (int i = 0; i < DBH; ++i) {
+    dk[i] = f32x16{};
+    dv[i] = f32x16{};
+  }
+
+  int roff[8];  // Q / dO tile rows (A operand of S, dP): row l32, chunk dh*DH/8 + 2*kk + h
+#pragma unroll
+  for (int kl = 0; kl < 8; ++kl) roff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz(l32)) << 4) + dh * DH * 2;
+  int toffA[4], toffB[4];  // Q / dO tiles read transposed (A operands of dK^T, dV^T)
+  {
+    const int t16 = lane & 15;
+    const int half16 = (lane >> 4) & 1;
+    const int rA = 4 * h + (t16 >> 2);
+    const int rB = rA + 8;
+#pragma unroll
+    for (int dl = 0; dl < 4; ++dl) {
+      const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
+      toffA[dl] = rA * (2 * D) + ((c ^ swz(rA)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
+      toffB[dl] = rB * (2 * D) + ((c ^ swz(rB)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
+    }
+  }
+  char GFA_LDS* xmine = xch + wave * XCH + lane * 16;
+  const char GFA_LDS* xpart = xch + (wave ^ 1) * XCH + lane * 16;
+
+  auto tile_src = [&](int it, const uint16_t* base, const RowView& v, int& q_start) {
+    const int r = it / nqt;
+    const int qt = qt_lo + it % nqt;
+    q_start = qt * BQ;
+    return base + (int64_t)b * v.sb + (int64_t)(kvh * p.R + r) * v.sh;
+  };
+
+  if (it_lo < it_hi) {
+    int qs0;
+    const uint16_t* qb = tile_src(it_lo, p.q, p.qv, qs0);
+    const uint16_t* db = tile_src(it_lo, p.dout, p.dov, qs0);
+    load_tile_async<D, BQ, NW>(qb, p.qv.sn, qs0, p.N, smem, wave, lane);
+    load_tile_async<D, BQ, NW>(db, p.dov.sn, qs0, p.N, smem + 2 * TILE, wave, lane);
+  }
+
+  for (int it = it_lo; it < it_hi; ++it) {
+    const int cur = (it - it_lo) & 1;
+    barrier_tile();
+    if (it + 1 < it_hi) {
+      int qs1;
+      const uint16_t* qb = tile_src(it + 1, p.q, p.qv, qs1);
+      const uint16_t* db = tile_src(it + 1, p.dout, p.dov, qs1);
+      load_tile_async<D, BQ, NW>(qb, p.qv.sn, qs1, p.N, smem + (cur ^ 1) * TILE, wave, lane);
+      load_tile_async<D, BQ, NW>(db, p.dov.sn, qs1, p.N, smem + (2 + (cur ^ 1)) * TILE, wave, lane);
+    }
+    const int head = kvh * p.R + it / nqt;
+    const int q0 = (qt_lo + it % nqt) * BQ;
+    const bool live = active && q0 < vis_hi && q0 + BQ > vis_lo;
+    const char GFA_LDS* qt = smem + cur * TILE;
+    const char GFA_LDS* dt = smem + (2 + cur) * TILE;
+
+    f32x16 s[SB], dp[SB];
+    if (live) {
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+        s[sb] = mma_chain_lds<IS_BF16, KTH, 4>(qt, roff, sb * 32 * (2 * D), kf);
+        dp[sb] = mma_chain_lds<IS_BF16, KTH, 4>(dt, roff, sb * 32 * (2 * D), vf);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 vs = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
+          const f32x4 vd = {dp[sb][4 * j], dp[sb][4 * j + 1], dp[sb][4 * j + 2], dp[sb][4 * j + 3]};
+          *reinterpret_cast<f32x4 GFA_LDS*>(xmine + (sb * 4 + j) * 1024) = vs;
+          *reinterpret_cast<f32x4 GFA_LDS*>(xmine + XHALF + (sb * 4 + j) * 1024) = vd;
+        }
+      }
+    }
+    barrier_lds();
+    if (!live) continue;
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 vs = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + (sb * 4 + j) * 1024);
+        const f32x4 vd = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + XHALF + (sb * 4 + j) * 1024);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[sb][4 * j + e] = s[sb][4 * j + e] + vs[e];
+          dp[sb][4 * j + e] = dp[sb][4 * j + e] + vd[e];
+        }
+      }
+    }
+
+    // ---- P and dS on the key lanes; rows (queries) are per-register ----
+    const bool need_mask = !(pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
+    const float* lse_row = p.lse + ((int64_t)b * p.Hq + head) * p.N;
+    const float* del_row = p.delta + ((int64_t)b * p.Hq + head) * p.N;
+    i16x8 pb[BQ / 16], dsb[BQ / 16];
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int qq = q0 + sb * 32 + 8 * g + 4 * h;  // rows qq .. qq+3 of this lane
+        f32x4 lse4, del4;
+        if (qq + 3 < p.N) {
+          lse4 = *reinterpret_cast<const f32x4*>(lse_row + qq);
+          del4 = *reinterpret_cast<const f32x4*>(del_row + qq);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int qe = min(qq + e, p.N - 1);
+            lse4[e] = lse_row[qe];
+            del4[e] = del_row[qe];
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          float pv = fast_exp2(s[sb][r] * p.scale_log2 - lse4[e] * kLog2e);
+          float ds = pv * (dp[sb][r] - del4[e]);
+          if (need_mask) {
+            const int qi = qq + e;
+            bool ok = key < p.N && qi < p.N;
+            if (p.causal) ok = ok && key <= qi;
+            if (swa) ok = ok && (qi - key) < p.window;
+            pv = ok ? pv : 0.f;
+            ds = ok ? ds : 0.f;
+          }
+          pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
+          dsb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(ds);
+        }
+      }
+    }
+
+    // ---- dV^T[half] += dO^T[half] P ; dK^T[half] += Q^T[half] dS ----
+#pragma unroll
+    for (int ks = 0; ks < BQ / 16; ++ks) {
+#pragma unroll
+      for (int db = 0; db < DBH; ++db) {
+        const int imm = ks * 16 * (2 * D) + 256 * (db >> 2);
+        const i16x4 dlo = lds_read_tr(dt, toffA[db & 3] + imm);
+        const i16x4 dhi = lds_read_tr(dt, toffB[db & 3] + imm);
+        const i16x8 ad = {dlo[0], dlo[1], dlo[2], dlo[3], dhi[0], dhi[1], dhi[2], dhi[3]};
+        dv[db] = mma32<IS_BF16>(ad, pb[ks], dv[db]);
+        const i16x4 qlo = lds_read_tr(qt, toffA[db & 3] + imm);
+        const i16x4 qhi = lds_read_tr(qt, toffB[db & 3] + imm);
+        const i16x8 aq = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
+        dk[db] = mma32<IS_BF16>(aq, dsb[ks], dk[db]);
+      }
+    }
+  }
+
+  // ---- epilogue: lane = key, registers = head-dim rows 32*db + 8*g + 4*h + e ----
+  if (active && key < p.N) {
+    if (p.q_splits == 1) {
+      uint16_t* dkrow = p.dk + (int64_t)b * p.dkv.sb + (int64_t)kvh * p.dkv.sh + (int64_t)key * p.dkv.sn + dh * DH;
+      uint16_t* dvrow = p.dv + (int64_t)b * p.dvv.sb + (int64_t)kvh * p.dvv.sh + (int64_t)key * p.dvv.sn + dh * DH;
+#pragma unroll
+      for (int db = 0; db < DBH; ++db) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          i16x4 k4, v4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            k4[e] = to16<IS_BF16>(dk[db][4 * g + e] * p.scale);
+            v4[e] = to16<IS_BF16>(dv[db][4 * g + e]);
+          }
+          *reinterpret_cast<i16x4*>(dkrow + db * 32 + 8 * g + 4 * h) = k4;
+          *reinterpret_cast<i16x4*>(dvrow + db * 32 + 8 * g + 4 * h) = v4;
+        }
+      }
+    } else {
+      // fp32 partials [split][dk|dv][b][kvh][key][d], dK already scaled.
+      const int64_t plane = (int64_t)p.B * p.Hkv * p.N * D;
+      const int64_t rowoff = (((int64_t)b * p.Hkv + kvh) * p.N + key) * D + dh * DH;
+      float* pk = p.part + (int64_t)split * 2 * plane + rowoff;
+      float* pv = pk + plane;
+#pragma unroll
+      for (int db = 0; db < DBH; ++db) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 k4 = {dk[db][4 * g] * p.scale, dk[db][4 * g + 1] * p.scale, dk[db][4 * g + 2] * p.scale,
+                            dk[db][4 * g + 3] * p.scale};
+          const f32x4 v4 = {dv[db][4 * g], dv[db][4 * g + 1], dv[db][4 * g + 2], dv[db][4 * g + 3]};
+          *reinterpret_cast<f32x4*>(pk + db * 32 + 8 * g + 4 * h) = k4;
+          *reinterpret_cast<f32x4*>(pv + db * 32 + 8 * g + 4 * h) = v4;
+        }
+      }
+    }
+  }
+}
+
+// dK/dV = sum over q_splits of the fp32 partials, in split order, cast to the input dtype.
+// One thread converts 8 consecutive head-dim elements of one (tensor, b, kvh, key) row.
+template <bool IS_BF16>
+__global__ __launch_bounds__(256) void dkv_reduce_kernel(const BwdDkvParams p, int D) {
+  const int64_t plane = (int64_t)p.B * p.Hkv * p.N * D;
+  const int64_t n8 = 2 * plane / 8;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n8) return;
+  const int64_t e0 = i * 8;
+  const int which = e0 >= plane ? 1 : 0;
+  const int64_t off = e0 - which * plane;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int s = 0; s < p.q_splits; ++s) {
+    const float* src = p.part + (int64_t)s * 2 * plane + which * plane + off;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src);
+    const f32x4 c = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[e] += a[e];
+      acc[4 + e] += c[e];
+    }
+  }
+  const int d = (int)(off % D);
+  int64_t rest = off / D;
+  const int key = (int)(rest % p.N);
+  rest /= p.N;
+  const int kvh = (int)(rest % p.Hkv);
+  const int b = (int)(rest / p.Hkv);
+  const RowView& v = which ? p.dvv : p.dkv;
+  uint16_t* dst = (which ? p.dv : p.dk) + (int64_t)b * v.sb + (int64_t)kvh * v.sh + (int64_t)key * v.sn + d;
+  i16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = to16<IS_BF16>(acc[e]);
+  *reinterpret_cast<i16x8*>(dst) = o;
+}
+
+template <int D, int BQ, bool IS_BF16, int NW>
+static hipError_t launch_dkv_t(const BwdDkvParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW>), dim3(p.nblocks), dim3(NW * 64), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, bool bf16, hipStream_t stream) {
+  if (D == 512 && bq == 32) return bf16 ? launch_dkv_t<512, 32, true, 4>(p, stream) : launch_dkv_t<512, 32, false, 4>(p, stream);
+  if (D == 256 && bq == 32) return bf16 ? launch_dkv_t<256, 32, true, 4>(p, stream) : launch_dkv_t<256, 32, false, 4>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_dkv_reduce(const BwdDkvParams& p, int D, bool bf16, hipStream_t stream) {
+  const int64_t n8 = 2 * (int64_t)p.B * p.Hkv * p.N * D / 8;
+  const int blocks = (int)((n8 + 255) / 256);
+  if (bf16) {
+    hipLaunchKernelGGL(dkv_reduce_kernel<true>, dim3(blocks), dim3(256), 0, stream, p, D);
+  } else {
+    hipLaunchKernelGGL(dkv_reduce_kernel<false>, dim3(blocks), dim3(256), 0, stream, p, D);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace gfa

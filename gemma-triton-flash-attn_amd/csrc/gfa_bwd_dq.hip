@@ -1,0 +1,241 @@
+// GQA flash-attention backward, dQ kernel with the fused delta prologue (hot-path row R2).
+//
+// Semantics follow /root/reference/flash_attn/attention.py:687-797 run with
+// STORE_DELTA=True (launch at 1506-1523):
+//   delta_i = sum_d dO_id * O_id                        (fp32, stored for the dKV kernel)
+//   P_ij    = exp2(s*log2e * q_i.k_j - LSE_i*log2e)      (masked -> 0)
+//   dS_ij   = P_ij * (dO_i.v_j - delta_i)                 (masked -> 0, cast to input dtype)
+//   dQ_i    = s * sum_j dS_ij k_j
+//
+// MI355X design: the same wave-pair decomposition as the forward kernel. A pair owns 32
+// query rows of one head; each wave keeps its head-dim half of Q and dO in VGPRs (B
+// operands of S^T = K Q^T and dP^T = V dO^T, lane = query), computes partial S^T and dP^T
+// over its half, and swaps them with the partner through LDS. P^T and dS^T then live on
+// the query lanes with per-lane LSE and delta, and dQ^T[half] += K^T[half] dS^T reads its
+// A operand with ds_read_b64_tr_b16 from the same row-major K tile that fed S^T. K and V
+// tiles are double-buffered in LDS via global_load_lds.
+#include "gfa_common.h"
+#include "gfa_params.h"
+#include "gfa_launch.h"
+
+namespace gfa {
+
+template <int D, int BKV, bool IS_BF16, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p) {
+  constexpr int DH = D / 2;
+  constexpr int KTH = DH / 16;
+  constexpr int DBH = DH / 32;
+  constexpr int SB = BKV / 32;
+  constexpr int TILE = BKV * D * 2;
+  constexpr int XHALF = SB * 16 * 64 * 4;  // one f32x16 per score block per lane
+  constexpr int XCH = 2 * XHALF;          // S^T and dP^T partials
+  static_assert(BKV % 32 == 0, "BKV must be a multiple of 32");
+  static_assert(DH % 128 == 0, "head dim must be 256 or 512");
+
+  __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NW * XCH];
+  char GFA_LDS* smem = (char GFA_LDS*)smem_raw;
+  char GFA_LDS* xch = smem + 4 * TILE;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int unit = wave >> 1;
+  const int dh = wave & 1;
+  const int h = lane >> 5;
+  const int l32 = lane & 31;
+
+  int lid = xcd_remap(blockIdx.x, p.g.nblocks, p.g.n_hg);
+  const int hg = lid % p.g.n_hg;
+  lid /= p.g.n_hg;
+  const int kvh = lid % p.Hkv;
+  lid /= p.Hkv;
+  const int b = lid % p.B;
+  lid /= p.B;
+  const int qsb = p.causal ? (p.g.n_qsb - 1 - lid) : lid;
+
+  const int head = kvh * p.R + hg * p.g.hpw + (unit % p.g.hpw);
+  const int q0 = (qsb * p.g.qbw + unit / p.g.hpw) * 32;
+  const int wg_q_lo = qsb * p.g.qbw * 32;
+  const int wg_q_hi = min(p.N, wg_q_lo + p.g.qbw * 32);
+
+  const bool swa = p.causal && p.window > 0;
+  int k_lo = 0, k_hi = p.N;
+  if (p.causal) {
+    k_hi = wg_q_hi;
+    if (swa) k_lo = max(0, wg_q_lo - p.window + 1);
+  }
+  const int t_lo = k_lo / BKV;
+  const int t_hi = (k_hi + BKV - 1) / BKV;
+
+  const bool active = q0 < p.N;
+  const int q_last = q0 + 31;
+  int vis_lo = 0, vis_hi = p.N, all_lo = 0, all_hi = p.N;
+  if (p.causal) {
+    vis_hi = min(p.N, q_last + 1);
+    all_hi = min(p.N, q0 + 1);
+    if (swa) {
+      vis_lo = max(0, q0 - p.window + 1);
+      all_lo = q_last - p.window + 1;
+    }
+  }
+
+  const int q = q0 + l32;
+  const int qrow = min(q, p.N - 1);
+  // ---- Q and dO halves (B operands), resident; delta prologue ----
+  i16x8 qf[KTH], df[KTH];
+  float dpart = 0.f;
+  {
+    const uint16_t* qr = p.q + (int64_t)b * p.qv.sb + (int64_t)head * p.qv.sh + (int64_t)qrow * p.qv.sn + dh * DH + 8 * h;
+    const uint16_t* dr = p.dout + (int64_t)b * p.dov.sb + (int64_t)head * p.dov.sh + (int64_t)qrow * p.dov.sn + dh * DH + 8 * h;
+    const uint16_t* orow = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh + (int64_t)qrow * p.ov.sn + dh * DH + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < KTH; ++kk) {
+      qf[kk] = *reinterpret_cast<const i16x8*>(qr + 16 * kk);
+      df[kk] = *reinterpret_cast<const i16x8*>(dr + 16 * kk);
+      const i16x8 of = *reinterpret_cast<const i16x8*>(orow + 16 * kk);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dpart += from16<IS_BF16>(df[kk][e]) * from16<IS_BF16>(of[e]);
+    }
+  }
+  dpart += __shfl_xor(dpart, 32);
+  // Pair exchange of the two head-dim halves of delta (through the exchange area).
+  *reinterpret_cast<float GFA_LDS*>(xch + wave * XCH + lane * 4) = dpart;
+  barrier_lds();
+  const float delta = dpart + *reinterpret_cast<const float GFA_LDS*>(xch + (wave ^ 1) * XCH + lane * 4);
+  if (active && q < p.N && dh == 0 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.N + q] = delta;
+  const float lse_log2 = p.lse[((int64_t)b * p.Hq + head) * p.N + qrow] * kLog2e;
+
+  f32x16 acc[DBH];
+#pragma unroll
+  for (int i = 0; i < DBH; ++i) acc[i] = f32x16{};
+
+  int koff[8];
+#pragma unroll
+  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz(l32)) << 4) + dh * DH * 2;
+  int toffA[4], toffB[4];  // K tile read transposed (A operand of dQ^T = K^T dS^T)
+  {
+    const int t16 = lane & 15;
+    const int half16 = (lane >> 4) & 1;
+    const int rA = 4 * h + (t16 >> 2);
+    const int rB = rA + 8;
+#pragma unroll
+    for (int dl = 0; dl < 4; ++dl) {
+      const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
+      toffA[dl] = rA * (2 * D) + ((c ^ swz(rA)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
+      toffB[dl] = rB * (2 * D) + ((c ^ swz(rB)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
+    }
+  }
+  char GFA_LDS* xmine = xch + wave * XCH + lane * 16;
+  const char GFA_LDS* xpart = xch + (wave ^ 1) * XCH + lane * 16;
+
+  const uint16_t* kbase = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh;
+  const uint16_t* vbase = p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh;
+
+  barrier_lds();  // everyone has read the delta exchange before it is overwritten
+  if (t_lo < t_hi) {
+    load_tile_async<D, BKV, NW>(kbase, p.kv.sn, t_lo * BKV, p.N, smem, wave, lane);
+    load_tile_async<D, BKV, NW>(vbase, p.vv.sn, t_lo * BKV, p.N, smem + 2 * TILE, wave, lane);
+  }
+
+  for (int t = t_lo; t < t_hi; ++t) {
+    const int cur = (t - t_lo) & 1;
+    barrier_tile();
+    if (t + 1 < t_hi) {
+      load_tile_async<D, BKV, NW>(kbase, p.kv.sn, (t + 1) * BKV, p.N, smem + (cur ^ 1) * TILE, wave, lane);
+      load_tile_async<D, BKV, NW>(vbase, p.vv.sn, (t + 1) * BKV, p.N, smem + (2 + (cur ^ 1)) * TILE, wave, lane);
+    }
+    const int k0 = t * BKV;
+    const bool live = active && k0 < vis_hi && k0 + BKV > vis_lo;
+    const char GFA_LDS* kt = smem + cur * TILE;
+    const char GFA_LDS* vt = smem + (2 + cur) * TILE;
+
+    f32x16 s[SB], dp[SB];
+    if (live) {
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+        s[sb] = mma_chain_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
+        dp[sb] = mma_chain_lds<IS_BF16, KTH, 4>(vt, koff, sb * 32 * (2 * D), df);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 vs = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
+          const f32x4 vd = {dp[sb][4 * j], dp[sb][4 * j + 1], dp[sb][4 * j + 2], dp[sb][4 * j + 3]};
+          *reinterpret_cast<f32x4 GFA_LDS*>(xmine + (sb * 4 + j) * 1024) = vs;
+          *reinterpret_cast<f32x4 GFA_LDS*>(xmine + XHALF + (sb * 4 + j) * 1024) = vd;
+        }
+      }
+    }
+    barrier_lds();
+    if (!live) continue;
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 vs = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + (sb * 4 + j) * 1024);
+        const f32x4 vd = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + XHALF + (sb * 4 + j) * 1024);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[sb][4 * j + e] = s[sb][4 * j + e] + vs[e];
+          dp[sb][4 * j + e] = dp[sb][4 * j + e] + vd[e];
+        }
+      }
+    }
+
+    const bool need_mask = !(k0 + BKV <= all_hi && k0 >= all_lo);
+    i16x8 dsb[BKV / 16];
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float pv = fast_exp2(s[sb][r] * p.scale_log2 - lse_log2);
+        float ds = pv * (dp[sb][r] - delta);
+        if (need_mask) {
+          const int key = k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          bool ok = key < p.N;
+          if (p.causal) ok = ok && key <= q;
+          if (swa) ok = ok && (q - key) < p.window;
+          ds = ok ? ds : 0.f;
+        }
+        dsb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(ds);
+      }
+    }
+
+#pragma unroll
+    for (int ks = 0; ks < BKV / 16; ++ks) {
+#pragma unroll
+      for (int db = 0; db < DBH; ++db) {
+        const int imm = ks * 16 * (2 * D) + 256 * (db >> 2);
+        const i16x4 lo = lds_read_tr(kt, toffA[db & 3] + imm);
+        const i16x4 hi = lds_read_tr(kt, toffB[db & 3] + imm);
+        const i16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc[db] = mma32<IS_BF16>(a, dsb[ks], acc[db]);
+      }
+    }
+  }
+
+  if (active && q < p.N) {
+    uint16_t* dqrow = p.dq + (int64_t)b * p.dqv.sb + (int64_t)head * p.dqv.sh + (int64_t)q * p.dqv.sn + dh * DH;
+#pragma unroll
+    for (int db = 0; db < DBH; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        i16x4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[db][4 * g + e] * p.scale);
+        *reinterpret_cast<i16x4*>(dqrow + db * 32 + 8 * g + 4 * h) = o4;
+      }
+    }
+  }
+}
+
+template <int D, int BKV, bool IS_BF16, int NW>
+static hipError_t launch_dq_t(const BwdDqParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_dq(const BwdDqParams& p, int D, int bkv, bool bf16, hipStream_t stream) {
+  if (D == 512 && bkv == 32) return bf16 ? launch_dq_t<512, 32, true, 4>(p, stream) : launch_dq_t<512, 32, false, 4>(p, stream);
+  if (D == 256 && bkv == 32) return bf16 ? launch_dq_t<256, 32, true, 4>(p, stream) : launch_dq_t<256, 32, false, 4>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace gfa

@@ -1,0 +1,75 @@
+// Kernel parameter blocks shared by the launchers and the device kernels.
+// All strides are in elements; the head dimension is always unit-stride.
+#pragma once
+#include <stdint.h>
+
+namespace gfa {
+
+// Row addressing of one (B, H, N, D) tensor: element (b, h, n, d) lives at
+// base + b * sb + h * sh + n * sn + d.
+struct RowView {
+  int64_t sb, sh, sn;
+};
+
+// Work decomposition shared by the forward and dQ kernels: a workgroup owns
+// NWAVES (head, 32-query block) pairs of one KV head: `hpw` heads x `qbw` query blocks.
+struct QGrid {
+  int hpw;    // query heads per workgroup (divides R)
+  int qbw;    // 32-row query blocks per workgroup (hpw * qbw == NWAVES)
+  int n_hg;   // R / hpw head groups per KV head
+  int n_qsb;  // ceil(N / (32 * qbw)) query super-blocks
+  int nblocks;
+};
+
+struct FwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* lse;  // (B, Hq, N) contiguous, natural log; may be null when store_lse == 0
+  RowView qv, kv, vv, ov;
+  int B, Hq, Hkv, N, R;
+  int causal;
+  int window;        // 0 = no sliding window; only honoured when causal
+  float scale_log2;  // softmax scale * log2(e)
+  int store_lse;
+  QGrid g;
+};
+
+struct BwdDqParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;
+  const uint16_t* dout;
+  const float* lse;  // (B, Hq, N)
+  float* delta;      // (B, Hq, N), written: rowsum(dO * O)
+  uint16_t* dq;
+  RowView qv, kv, vv, ov, dov, dqv;
+  int B, Hq, Hkv, N, R;
+  int causal, window;
+  float scale;       // softmax scale (applied to dQ at the end)
+  float scale_log2;  // scale * log2(e)
+  QGrid g;
+};
+
+struct BwdDkvParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* dout;
+  const float* lse;
+  const float* delta;
+  uint16_t* dk;      // written directly when q_splits == 1
+  uint16_t* dv;
+  float* part;       // fp32 partials [q_splits][2][B][Hkv][N][D] when q_splits > 1
+  RowView qv, kv, vv, dov, dkv, dvv;
+  int B, Hq, Hkv, N, R;
+  int causal, window;
+  float scale, scale_log2;
+  int q_splits;
+  int n_kb;          // number of key blocks (each WKV keys wide)
+  int nblocks;
+};
+
+}  // namespace gfa

@@ -1,0 +1,101 @@
+"""HEAD_DIM-keyed kernel-config registry.
+
+The reference keeps its tile choices as if/else tables keyed on HEAD_DIM inside the
+launch code (/root/reference/flash_attn/attention.py:561-579 inference forward,
+1445-1451 training forward, 1498-1504 dQ, 1536-1564 dKV, 1576-1587 Q_SPLITS). Here the
+same role is one explicit table. Each entry names the tiles of the three gfx950 kernels;
+every kernel works on wave pairs that split the head dim, 32 rows per pair.
+
+The C library holds the same table (csrc/gfa_api.hip, kRegistry); ``gfa_config`` reports
+what the library will use and the tests assert the two agree.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+NUM_CUS = 256  # MI355X compute units; the Q-split target is one workgroup per CU
+
+
+@dataclass(frozen=True)
+class KernelConfig:
+    head_dim: int
+    fwd_block_kv: int   # keys per LDS tile in the forward
+    fwd_waves: int      # waves per forward workgroup (pairs = waves / 2)
+    dq_block_kv: int
+    dq_waves: int
+    dkv_block_q: int    # queries per LDS tile in the dKV kernel
+    dkv_waves: int
+    fwd_block_kv_options: tuple = ()  # other built forward tile widths (BLOCK_KV override)
+
+
+REGISTRY: dict[int, KernelConfig] = {
+    512: KernelConfig(512, fwd_block_kv=32, fwd_waves=4, dq_block_kv=32, dq_waves=4, dkv_block_q=32, dkv_waves=4,
+                      fwd_block_kv_options=(32,)),
+    256: KernelConfig(256, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dkv_block_q=32, dkv_waves=4,
+                      fwd_block_kv_options=(32, 64)),
+}
+
+SUPPORTED_HEAD_DIMS = tuple(sorted(REGISTRY))
+
+
+def lookup(head_dim: int) -> KernelConfig:
+    try:
+        return REGISTRY[head_dim]
+    except KeyError:
+        raise ValueError(f"head_dim={head_dim} is not in the registry {SUPPORTED_HEAD_DIMS}") from None
+
+
+def _pow2_divisor_le(r: int, cap: int) -> int:
+    x = 1
+    while x * 2 <= cap and r % (x * 2) == 0:
+        x *= 2
+    return x
+
+
+def query_grid(batch: int, heads_q: int, heads_kv: int, seq_len: int, waves: int) -> dict:
+    """Workgroup decomposition of the forward / dQ kernels (pack-GQA).
+
+    A workgroup holds waves/2 wave pairs; each pair owns 32 query rows of one query head.
+    The pairs are ``hpw`` heads of one KV head times ``qbw`` neighbouring 32-row blocks.
+    """
+    r = heads_q // heads_kv
+    units = waves // 2
+    hpw = _pow2_divisor_le(r, units)
+    qbw = units // hpw
+    n_qsb = -(-seq_len // (32 * qbw))
+    return {"hpw": hpw, "qbw": qbw, "block_q": 32 * qbw, "n_hg": r // hpw, "n_qsb": n_qsb,
+            "nblocks": n_qsb * batch * heads_kv * (r // hpw)}
+
+
+def q_splits_for(batch: int, heads_kv: int, seq_len: int, waves: int) -> int:
+    """Smallest of {1, 2, 4, 8} giving at least one dKV workgroup per CU.
+
+    Same intent as the reference's Q_SPLITS rule (attention.py:1576-1587): split each key
+    block's query range only when the raw grid cannot fill the GPU.
+    """
+    keys_per_wg = 32 * (waves // 2)
+    grid = -(-seq_len // keys_per_wg) * batch * heads_kv
+    qs = 1
+    while qs < 8 and grid * qs < NUM_CUS:
+        qs *= 2
+    return qs
+
+
+def get_config(batch: int, heads_q: int, heads_kv: int, seq_len: int, head_dim: int) -> dict:
+    """Everything the library decides for one problem (same keys as ``gfa_config``)."""
+    c = lookup(head_dim)
+    fq = query_grid(batch, heads_q, heads_kv, seq_len, c.fwd_waves)
+    dq = query_grid(batch, heads_q, heads_kv, seq_len, c.dq_waves)
+    return {
+        "head_dim": head_dim,
+        "fwd_block_q": fq["block_q"],
+        "fwd_block_kv": c.fwd_block_kv,
+        "fwd_waves": c.fwd_waves,
+        "dq_block_q": dq["block_q"],
+        "dq_block_kv": c.dq_block_kv,
+        "dq_waves": c.dq_waves,
+        "dkv_block_kv": 32 * (c.dkv_waves // 2),
+        "dkv_block_q": c.dkv_block_q,
+        "dkv_waves": c.dkv_waves,
+        "q_splits": q_splits_for(batch, heads_kv, seq_len, c.dkv_waves),
+    }

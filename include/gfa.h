@@ -1,0 +1,133 @@
+/*
+ * gfa.h - C ABI of the MI355X (gfx950) GQA flash-attention engine.
+ *
+ * Plain C: raw device pointers, element strides and sizes, a hipStream_t passed as
+ * void*. No framework types cross this boundary. The library never allocates, frees
+ * or synchronises; every call is stream-ordered on the caller's stream and device.
+ *
+ * Tensor layout: q/o/do/dq are (B, Hq, N, D); k/v/dk/dv are (B, Hkv, N, D); every
+ * tensor is addressed through its own (batch, head, row) element strides and must have
+ * a unit-stride head dimension and 16-byte aligned rows. lse/delta are contiguous
+ * (B, Hq, N) float32. Query head h reads KV head h / (Hq / Hkv) (contiguous groups).
+ *
+ * The entry points replace the reference's Triton launch sites (file:line in
+ * /root/reference, zzhhjjj/gemma-triton-flash-attn):
+ *   gfa_fwd          flash_attn/attention.py:1454-1468 (_flash_attn_gqa_kernel launch,
+ *                    STORE_LSE=True, training forward) and attention.py:589-601
+ *                    (inference forward, STORE_LSE=False -> lse == NULL)
+ *   gfa_bwd          flash_attn/attention.py:1506-1620 (dQ kernel with fused delta,
+ *                    then the pack-GQA dKV kernel with its Q_SPLITS partial sums)
+ *   gfa_config       the HEAD_DIM-keyed tile tables at attention.py:561-579, 1445-1451,
+ *                    1498-1504, 1536-1564 and the Q_SPLITS choice at 1576-1587
+ *   gfa_bwd_workspace_size
+ *                    sizing of the (2,)+k.shape pre-zeroed buffer of attention.py:1594-1600
+ *                    (here: fp32 partials, owned by the caller)
+ */
+#ifndef GFA_H_
+#define GFA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GFA_VERSION 100 /* 1.0.0 */
+
+typedef enum {
+  GFA_DTYPE_FP16 = 0,
+  GFA_DTYPE_BF16 = 1
+} gfa_dtype;
+
+typedef enum {
+  GFA_OK = 0,
+  GFA_ERR_INVALID_ARGUMENT = 1, /* shape / stride / dtype / alignment / head-dim problem */
+  GFA_ERR_UNSUPPORTED = 2,      /* valid request outside the built kernel set          */
+  GFA_ERR_WORKSPACE = 3,        /* workspace missing or too small                      */
+  GFA_ERR_LAUNCH = 4            /* the HIP runtime rejected a kernel launch            */
+} gfa_status;
+
+/* Element strides (batch, head, row) of one 4-D tensor; the head-dim stride is 1. */
+typedef struct {
+  int64_t batch, head, row;
+} gfa_strides;
+
+typedef struct {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse; /* (B, Hq, N) natural-log logsumexp; NULL = inference (not stored) */
+  gfa_strides q_strides, k_strides, v_strides, o_strides;
+  int32_t batch, heads_q, heads_kv, seq_len, head_dim;
+  int32_t causal;      /* 0 / 1 */
+  int32_t window;      /* sliding window; 0 = off; honoured only when causal; >= seq_len -> off */
+  float scale;         /* softmax scale; the reference uses 1/sqrt(head_dim) */
+  int32_t dtype;       /* gfa_dtype, shared by q/k/v/o */
+  int32_t block_kv;    /* 0 = registry default, else a built tile width */
+  void* stream;        /* hipStream_t */
+} gfa_fwd_args;
+
+typedef struct {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  const float* lse; /* from gfa_fwd */
+  float* delta;     /* (B, Hq, N) scratch written by the dQ kernel: rowsum(dO * O) */
+  void* dq;
+  void* dk;
+  void* dv;
+  gfa_strides q_strides, k_strides, v_strides, o_strides, do_strides, dq_strides, dk_strides, dv_strides;
+  int32_t batch, heads_q, heads_kv, seq_len, head_dim;
+  int32_t causal, window;
+  float scale;
+  int32_t dtype;
+  int32_t q_splits;       /* 0 = registry choice, else 1, 2, 4 or 8 */
+  void* workspace;        /* >= gfa_bwd_workspace_size(...) bytes when q_splits > 1 */
+  size_t workspace_bytes;
+  void* stream;
+} gfa_bwd_args;
+
+/* Tile configuration the library uses for one problem (mirrors the Python registry). */
+typedef struct {
+  int32_t head_dim;
+  int32_t fwd_block_q;      /* query rows per forward workgroup */
+  int32_t fwd_block_kv;     /* keys per LDS tile */
+  int32_t fwd_waves;
+  int32_t dq_block_q;
+  int32_t dq_block_kv;
+  int32_t dq_waves;
+  int32_t dkv_block_kv;     /* keys per dKV workgroup */
+  int32_t dkv_block_q;      /* queries per LDS tile */
+  int32_t dkv_waves;
+  int32_t q_splits;
+} gfa_config_info;
+
+/* Forward: O (and LSE unless lse == NULL). Returns a gfa_status. */
+int gfa_fwd(const gfa_fwd_args* args);
+
+/* Backward: delta, dQ, then dK/dV (summing Q-split fp32 partials when q_splits > 1). */
+int gfa_bwd(const gfa_bwd_args* args);
+
+/* Workspace bytes gfa_bwd needs for the given problem and q_splits (0 = registry choice). */
+size_t gfa_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len, int32_t head_dim,
+                              int32_t causal, int32_t window, int32_t q_splits);
+
+/* Fill *out with the configuration used for this problem. Returns a gfa_status. */
+int gfa_config(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len, int32_t head_dim,
+               gfa_config_info* out);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* gfa_last_error(void);
+
+/* GFA_VERSION of the built library. */
+int gfa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GFA_H_ */

@@ -1,0 +1,176 @@
+"""CPU restatement of the reference's attention math: the parity oracle.
+
+TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module, and only as the checker. No engine code path
+calls it; the engine has no CPU path.
+
+What it restates (all paths under /root/reference, zzhhjjj/gemma-triton-flash-attn):
+  * op and masks: flash_attn/attention.py:611-619 (attention_gqa_ref: GQA by
+    repeat_interleave, scale 1/sqrt(D)), 622-642 (attention_swa_ref: key j visible to
+    query i iff j <= i and i - j < slide_size), 347-355 (kernel mask; the window only
+    applies when causal), 1441-1443 (window >= N is plain causal), 272 (query head h
+    reads KV head h * Hkv // Hq);
+  * forward outputs: 377 (O = acc / l), 382-388 (LSE in natural log);
+  * backward: 733-744 (delta = rowsum(dO * O) in fp32), 785-793 (P = exp(S - LSE),
+    dS = P * (dP - delta), dQ = scale * dS K), 1192-1202 (dV = P^T dO, dK = scale * dS^T Q,
+    summed over the query heads of a KV group).
+
+Two implementations of the same equations:
+  * ``forward`` / ``backward``: numpy float64, dense (N x N per head) - small cases and
+    golden vectors;
+  * ``forward_chunked`` / ``backward_chunked``: torch float32 on any device, query-chunked
+    so N = 32K fits - the large-shape check on the GPU box (a torch fp32 reference of the
+    same op, never the engine).
+
+Pinned by tests/test_oracle.py against: torch's scaled_dot_product_attention (math
+backend, float64) and its autograd for forward/backward, the committed golden vectors in
+tests/golden (written by that independent library path), finite differences, and
+closed forms (Q = 0 gives prefix / window means and LSE = ln |allowed|; window 1 gives
+O = V; GQA equals MHA on repeated K/V; shift invariance in K; convexity of O).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def allowed_mask(n: int, causal: bool, window: int = 0) -> np.ndarray:
+    """Boolean (N, N) mask: entry [i, j] is True when query i may attend key j."""
+    i = np.arange(n)[:, None]
+    j = np.arange(n)[None, :]
+    m = np.ones((n, n), dtype=bool)
+    if causal:
+        m &= j <= i
+        if window and 0 < window < n:
+            m &= (i - j) < window
+    return m
+
+
+def _default_scale(d: int, scale):
+    return 1.0 / math.sqrt(d) if scale is None else float(scale)
+
+
+def forward(q, k, v, causal=False, window=0, scale=None):
+    """O (B, Hq, N, D) and natural-log LSE (B, Hq, N), float64."""
+    q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+    B, Hq, N, D = q.shape
+    Hkv = k.shape[1]
+    sc = _default_scale(D, scale)
+    mask = allowed_mask(N, causal, window)
+    o = np.empty_like(q)
+    lse = np.empty((B, Hq, N))
+    for b in range(B):
+        for h in range(Hq):
+            g = h * Hkv // Hq
+            s = sc * (q[b, h] @ k[b, g].T)
+            s = np.where(mask, s, -np.inf)
+            mx = s.max(axis=1, keepdims=True)
+            p = np.exp(s - mx)
+            l = p.sum(axis=1, keepdims=True)
+            o[b, h] = (p / l) @ v[b, g]
+            lse[b, h] = (mx + np.log(l))[:, 0]
+    return o, lse
+
+
+def backward(q, k, v, do, causal=False, window=0, scale=None):
+    """dQ, dK, dV (float64) and delta = rowsum(dO * O) for the loss sum(O * dO)."""
+    q, k, v, do = (np.asarray(x, dtype=np.float64) for x in (q, k, v, do))
+    B, Hq, N, D = q.shape
+    Hkv = k.shape[1]
+    sc = _default_scale(D, scale)
+    o, lse = forward(q, k, v, causal, window, scale)
+    mask = allowed_mask(N, causal, window)
+    dq = np.zeros_like(q)
+    dk = np.zeros_like(k)
+    dv = np.zeros_like(v)
+    delta = (do * o).sum(axis=-1)
+    for b in range(B):
+        for h in range(Hq):
+            g = h * Hkv // Hq
+            s = sc * (q[b, h] @ k[b, g].T)
+            p = np.where(mask, np.exp(s - lse[b, h][:, None]), 0.0)
+            dp = do[b, h] @ v[b, g].T
+            ds = p * (dp - delta[b, h][:, None])
+            dq[b, h] = sc * (ds @ k[b, g])
+            dk[b, g] += sc * (ds.T @ q[b, h])
+            dv[b, g] += p.T @ do[b, h]
+    return dq, dk, dv, delta
+
+
+# ----------------------------------------------------------------------------------------
+# torch float32, query-chunked: the same equations for shapes too large for dense N x N.
+# ----------------------------------------------------------------------------------------
+
+def _chunk_mask(torch, q_lo, q_hi, n, causal, window, device):
+    i = torch.arange(q_lo, q_hi, device=device)[:, None]
+    j = torch.arange(n, device=device)[None, :]
+    m = torch.ones((q_hi - q_lo, n), dtype=torch.bool, device=device)
+    if causal:
+        m &= j <= i
+        if window and 0 < window < n:
+            m &= (i - j) < window
+    return m
+
+
+def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024):
+    """torch fp32 O and LSE for (B, H, N, D) tensors of any float dtype / device."""
+    import torch
+
+    B, Hq, N, D = q.shape
+    Hkv = k.shape[1]
+    sc = _default_scale(D, scale)
+    o = torch.empty((B, Hq, N, D), dtype=torch.float32, device=q.device)
+    lse = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device)
+    for b in range(B):
+        for g in range(Hkv):
+            kf = k[b, g].float().contiguous()
+            vf = v[b, g].float().contiguous()
+            kt = kf.t().contiguous()
+            for h in range(g * Hq // Hkv, (g + 1) * Hq // Hkv):
+                qf = q[b, h].float()
+                for lo in range(0, N, chunk):
+                    hi = min(N, lo + chunk)
+                    s = (qf[lo:hi] @ kt) * sc
+                    s = s.masked_fill(~_chunk_mask(torch, lo, hi, N, causal, window, q.device), float("-inf"))
+                    m = s.amax(dim=1, keepdim=True)
+                    p = torch.exp(s - m)
+                    l = p.sum(dim=1, keepdim=True)
+                    o[b, h, lo:hi] = (p @ vf) / l
+                    lse[b, h, lo:hi] = (m + torch.log(l))[:, 0]
+    return o, lse
+
+
+def backward_chunked(q, k, v, do, causal=False, window=0, scale=None, chunk=1024, o=None, lse=None):
+    """torch fp32 dQ, dK, dV, delta. ``o``/``lse`` may be passed to skip the recomputation."""
+    import torch
+
+    B, Hq, N, D = q.shape
+    Hkv = k.shape[1]
+    sc = _default_scale(D, scale)
+    if o is None or lse is None:
+        o, lse = forward_chunked(q, k, v, causal, window, scale, chunk)
+    dq = torch.empty((B, Hq, N, D), dtype=torch.float32, device=q.device)
+    dk = torch.zeros((B, Hkv, N, D), dtype=torch.float32, device=q.device)
+    dv = torch.zeros((B, Hkv, N, D), dtype=torch.float32, device=q.device)
+    delta = (do.float() * o.float()).sum(dim=-1)
+    for b in range(B):
+        for g in range(Hkv):
+            kf = k[b, g].float().contiguous()
+            vf = v[b, g].float().contiguous()
+            kt = kf.t().contiguous()
+            vt = vf.t().contiguous()
+            for h in range(g * Hq // Hkv, (g + 1) * Hq // Hkv):
+                qf = q[b, h].float()
+                dof = do[b, h].float()
+                for lo in range(0, N, chunk):
+                    hi = min(N, lo + chunk)
+                    mask = _chunk_mask(torch, lo, hi, N, causal, window, q.device)
+                    s = (qf[lo:hi] @ kt) * sc
+                    p = torch.exp(s - lse[b, h, lo:hi, None].float()).masked_fill(~mask, 0.0)
+                    dp = dof[lo:hi] @ vt
+                    ds = p * (dp - delta[b, h, lo:hi, None])
+                    dq[b, h, lo:hi] = (ds @ kf) * sc
+                    dk[b, g] += (ds.t().contiguous() @ qf[lo:hi]) * sc
+                    dv[b, g] += p.t().contiguous() @ dof[lo:hi]
+    return dq, dk, dv, delta

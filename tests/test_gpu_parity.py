@@ -1,0 +1,147 @@
+"""GPU parity of the HIP kernels against the oracle (float64 numpy on the exact same
+16-bit inputs) at sizes the oracle finishes in seconds, and against the golden vectors.
+
+Tolerances: O max-abs <= 1e-2 (fp16) / 2e-2 (bf16);
+dQ, dK, dV relative Frobenius error <= 5e-2. LSE is checked to 1e-2 absolute.
+"""
+from __future__ import annotations
+
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import make_inputs
+from oracle import attention_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+O_TOL = {torch.float16: 1e-2, torch.bfloat16: 2e-2}
+GRAD_TOL = 5e-2
+# Absolute floor (RMS per element) for gradients whose exact value is ~0 (e.g. window 1,
+# where dS = P * (dP - delta) cancels exactly): relative error is meaningless there.
+GRAD_ABS_RMS = 1e-3
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _rel(a, b):
+    """||a - b||_F / ||b||_F, with the denominator floored at GRAD_ABS_RMS * sqrt(numel)
+    so that an exactly-zero reference gradient is judged by absolute error."""
+    floor = GRAD_ABS_RMS * np.sqrt(b.size) / GRAD_TOL
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), floor))
+
+
+def _run(q, k, v, do, causal, window):
+    import gemma_triton_flash_attn_amd as gfa
+
+    qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    o = gfa.flash_attn_gqa_train(qq, kk, vv, causal=causal, slide_size=window)
+    o.backward(do)
+    torch.cuda.synchronize()
+    return o, qq.grad, kk.grad, vv.grad
+
+
+SMALL = [
+    # B, Hq, Hkv, N, D, causal, window, dtype
+    (1, 4, 1, 128, 512, True, 0, torch.bfloat16),
+    (1, 8, 1, 96, 512, True, 0, torch.float16),
+    (1, 2, 2, 70, 512, False, 0, torch.bfloat16),
+    (2, 4, 2, 100, 256, True, 0, torch.bfloat16),
+    (1, 4, 2, 160, 256, True, 48, torch.bfloat16),
+    (1, 2, 1, 200, 256, True, 33, torch.float16),
+    (1, 16, 2, 64, 256, True, 1, torch.bfloat16),
+    (1, 2, 1, 40, 256, True, 64, torch.bfloat16),   # window >= N -> causal
+    (1, 8, 8, 33, 256, False, 0, torch.float16),
+    (1, 4, 4, 1, 512, True, 0, torch.bfloat16),     # N = 1
+    (1, 6, 3, 31, 256, True, 0, torch.bfloat16),    # odd group size
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,causal,window,dtype", SMALL)
+def test_fwd_bwd_vs_oracle(B, Hq, Hkv, N, D, causal, window, dtype, device):
+    print(f"case B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal} window={window} {dtype}", flush=True)
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, dtype, device, seed=N + D)
+    o, dq, dk, dv = _run(q, k, v, do, causal, window)
+    o_ref, lse_ref = orc.forward(_np(q), _np(k), _np(v), causal, window)
+    dq_ref, dk_ref, dv_ref, _ = orc.backward(_np(q), _np(k), _np(v), _np(do), causal, window)
+    err_o = float(np.abs(_np(o) - o_ref).max())
+    errs = [_rel(_np(g), r) for g, r in ((dq, dq_ref), (dk, dk_ref), (dv, dv_ref))]
+    print(f"  O max-abs {err_o:.3e}  dQ/dK/dV rel {errs[0]:.3e} {errs[1]:.3e} {errs[2]:.3e}", flush=True)
+    assert err_o <= O_TOL[dtype]
+    assert max(errs) <= GRAD_TOL
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,causal,window,dtype", SMALL[:6])
+def test_lse_and_inference_path(B, Hq, Hkv, N, D, causal, window, dtype, device):
+    from gemma_triton_flash_attn_amd.attention import _forward
+
+    q, k, v, _ = make_inputs(B, Hq, Hkv, N, D, dtype, device, seed=7 + N)
+    scale = D ** -0.5
+    o, lse = _forward(q, k, v, causal, window if window < N else 0, scale, store_lse=True)
+    o_ref, lse_ref = orc.forward(_np(q), _np(k), _np(v), causal, window)
+    assert float(np.abs(_np(lse) - lse_ref).max()) <= 1e-2
+    import gemma_triton_flash_attn_amd as gfa
+
+    o_inf = gfa.attention_flash_gqa(q, k, v, causal=causal, slide_size=window)
+    torch.cuda.synchronize()
+    assert torch.equal(o_inf, o), "inference and training forward must agree bitwise"
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "d*_*.npz"))))
+def test_golden_vectors(path, device):
+    z = np.load(path)
+    B, Hq, Hkv, N, D, causal, window = (int(x) for x in z["meta"])
+    if D not in (256, 512):
+        pytest.skip("head dim outside the kernel set (oracle-only vector)")
+    print(f"golden {os.path.basename(path)}", flush=True)
+    q, k, v, do = (torch.from_numpy(z[n].view(np.int16)).view(torch.bfloat16).to(device) for n in ("q", "k", "v", "do"))
+    o, dq, dk, dv = _run(q, k, v, do, bool(causal), window)
+    assert float(np.abs(_np(o) - z["o"]).max()) <= O_TOL[torch.bfloat16]
+    for g, n in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+        assert _rel(_np(g), z[n].astype(np.float64)) <= GRAD_TOL, n
+
+
+def test_hf_strided_layout_matches_contiguous(device):
+    """(B, H, N, D) views of (B, N, H, D) storage (what transformers passes) give the same
+    bits as contiguous inputs, and O keeps the caller's layout."""
+    import gemma_triton_flash_attn_amd as gfa
+
+    args = (1, 8, 2, 96, 256, torch.bfloat16, device)
+    qs, ks, vs, dos = make_inputs(*args, seed=3, layout="bnhd")
+    qc, kc, vc, doc = (t.contiguous() for t in (qs, ks, vs, dos))
+    o1, g1 = _run(qs, ks, vs, dos, True, 40)[0], _run(qs, ks, vs, dos, True, 40)[1:]
+    o2, g2 = _run(qc, kc, vc, doc, True, 40)[0], _run(qc, kc, vc, doc, True, 40)[1:]
+    assert torch.equal(o1, o2)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+    o3 = gfa.attention_flash_gqa(qs, ks, vs, causal=True, slide_size=40)
+    assert o3.stride() == qs.stride()
+
+
+def test_deterministic(device):
+    q, k, v, do = make_inputs(1, 8, 2, 192, 512, torch.bfloat16, device, seed=11)
+    r1 = _run(q, k, v, do, True, 0)
+    r2 = _run(q, k, v, do, True, 0)
+    for a, b in zip(r1, r2):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("qs", [2, 4, 8])
+def test_q_splits_match(qs, device):
+    """Q-split fp32 partials + reduction agree with the single-split kernel."""
+    from gemma_triton_flash_attn_amd.attention import _backward, _forward
+
+    q, k, v, do = make_inputs(1, 8, 1, 256, 256, torch.bfloat16, device, seed=5)
+    o, lse = _forward(q, k, v, True, 0, 256 ** -0.5, store_lse=True)
+    ref = _backward(q, k, v, o, lse, do, True, 0, 256 ** -0.5, q_splits=1)
+    got = _backward(q, k, v, o, lse, do, True, 0, 256 ** -0.5, q_splits=qs)
+    torch.cuda.synchronize()
+    assert torch.equal(ref[0], got[0])  # dQ does not depend on the split
+    for a, b in zip(ref[1:3], got[1:3]):
+        assert _rel(_np(b), _np(a)) < 1e-2

@@ -1,0 +1,189 @@
+"""Pins the oracle (oracle/attention_oracle.py) before anything is compared against it.
+
+Checks, chosen so that a dropped term, a wrong sign/index or a transposed operand fails:
+  * torch scaled_dot_product_attention (math backend, float64) and its autograd - an
+    independent library implementation - on causal / sliding-window / full GQA cases;
+  * the committed golden vectors (written by that library path);
+  * finite differences of sum(O * dO) on tiny inputs;
+  * closed forms: Q = 0 -> prefix / window means with LSE = ln |allowed|, window 1 ->
+    O = V, N = 1, GQA == MHA on repeated K/V, shift invariance in K, convex rows,
+    Q = 0 -> dV_j = sum_{i sees j} dO_i / |allowed(i)|;
+  * the chunked torch fp32 variant against the float64 one.
+"""
+from __future__ import annotations
+
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+from oracle import attention_oracle as orc
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+CASES = [
+    # B, Hq, Hkv, N, D, causal, window
+    (1, 2, 2, 9, 4, False, 0),
+    (2, 4, 2, 13, 8, True, 0),
+    (1, 6, 2, 17, 8, True, 5),
+    (1, 8, 1, 11, 16, True, 1),
+    (1, 4, 4, 7, 4, True, 0),
+    (1, 2, 1, 12, 8, True, 64),  # window >= N -> plain causal
+]
+
+
+def _rand(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape)
+
+
+def _sdpa64(q, k, v, do, causal, window):
+    q, k, v, do = (torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in (q, k, v, do))
+    r = q.shape[1] // k.shape[1]
+    ke, ve = k.repeat_interleave(r, 1), v.repeat_interleave(r, 1)
+    n = q.shape[2]
+    i = torch.arange(n)[:, None]
+    j = torch.arange(n)[None, :]
+    m = torch.ones(n, n, dtype=torch.bool)
+    if causal:
+        m &= j <= i
+        if window and window < n:
+            m &= (i - j) < window
+    with sdpa_kernel(SDPBackend.MATH):
+        o = F.scaled_dot_product_attention(q, ke, ve, attn_mask=torch.zeros(n, n, dtype=torch.float64)
+                                           .masked_fill(~m, float("-inf"))[None, None])
+    (o * do.detach()).sum().backward()
+    return o.detach().numpy(), q.grad.numpy(), k.grad.numpy(), v.grad.numpy()
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,causal,window", CASES)
+def test_oracle_matches_torch_sdpa_fwd_bwd(B, Hq, Hkv, N, D, causal, window):
+    q, k, v, do = (_rand(s, i) for i, s in enumerate([(B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D), (B, Hq, N, D)]))
+    o_ref, dq_ref, dk_ref, dv_ref = _sdpa64(q, k, v, do, causal, window)
+    o, _ = orc.forward(q, k, v, causal, window)
+    dq, dk, dv, delta = orc.backward(q, k, v, do, causal, window)
+    np.testing.assert_allclose(o, o_ref, atol=1e-12, rtol=1e-10)
+    np.testing.assert_allclose(dq, dq_ref, atol=1e-11, rtol=1e-9)
+    np.testing.assert_allclose(dk, dk_ref, atol=1e-11, rtol=1e-9)
+    np.testing.assert_allclose(dv, dv_ref, atol=1e-11, rtol=1e-9)
+    np.testing.assert_allclose(delta, (do * o_ref).sum(-1), atol=1e-12)
+
+
+def _bits_to_f32(u16):
+    return (u16.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))))
+def test_oracle_matches_golden(path):
+    z = np.load(path)
+    B, Hq, Hkv, N, D, causal, window = (int(x) for x in z["meta"])
+    q, k, v, do = (_bits_to_f32(z[n]) for n in ("q", "k", "v", "do"))
+    o, lse = orc.forward(q, k, v, bool(causal), window)
+    dq, dk, dv, _ = orc.backward(q, k, v, do, bool(causal), window)
+    np.testing.assert_allclose(o, z["o"], atol=2e-6, rtol=1e-5)
+    np.testing.assert_allclose(lse, z["lse"], atol=2e-5, rtol=1e-5)
+    for got, name in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+        np.testing.assert_allclose(got, z[name], atol=2e-5, rtol=1e-4)
+
+
+def test_finite_differences():
+    B, Hq, Hkv, N, D = 1, 4, 2, 6, 3
+    q, k, v, do = (_rand(s, 10 + i) for i, s in enumerate([(B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D), (B, Hq, N, D)]))
+    for causal, window in ((True, 0), (True, 2), (False, 0)):
+        dq, dk, dv, _ = orc.backward(q, k, v, do, causal, window)
+
+        def loss(qq, kk, vv):
+            return float((orc.forward(qq, kk, vv, causal, window)[0] * do).sum())
+
+        eps = 1e-6
+        for arr, grad, which in ((q, dq, 0), (k, dk, 1), (v, dv, 2)):
+            for idx in [(0, 0, 0, 0), (0, 1, 3, 2), (0, arr.shape[1] - 1, N - 1, 1)]:
+                xp = [q.copy(), k.copy(), v.copy()]
+                xm = [q.copy(), k.copy(), v.copy()]
+                xp[which][idx] += eps
+                xm[which][idx] -= eps
+                fd = (loss(*xp) - loss(*xm)) / (2 * eps)
+                assert abs(fd - grad[idx]) < 1e-6, (causal, window, which, idx, fd, grad[idx])
+
+
+@pytest.mark.parametrize("causal,window", [(True, 0), (True, 3), (False, 0)])
+def test_zero_query_gives_means(causal, window):
+    B, Hq, Hkv, N, D = 1, 4, 2, 10, 5
+    q = np.zeros((B, Hq, N, D))
+    k = _rand((B, Hkv, N, D), 1)
+    v = _rand((B, Hkv, N, D), 2)
+    o, lse = orc.forward(q, k, v, causal, window)
+    for h in range(Hq):
+        g = h // 2
+        for i in range(N):
+            if causal:
+                lo = max(0, i - window + 1) if window else 0
+                js = range(lo, i + 1)
+            else:
+                js = range(N)
+            js = list(js)
+            np.testing.assert_allclose(o[0, h, i], v[0, g, js].mean(0), atol=1e-12)
+            assert abs(lse[0, h, i] - np.log(len(js))) < 1e-12
+    # Backward closed form at Q = 0: P is uniform over the allowed set.
+    do = _rand((B, Hq, N, D), 3)
+    _, _, dv, _ = orc.backward(q, k, v, do, causal, window)
+    mask = orc.allowed_mask(N, causal, window)
+    cnt = mask.sum(1)
+    expect = np.zeros((B, Hkv, N, D))
+    for h in range(Hq):
+        expect[0, h // 2] += (mask / cnt[:, None]).T @ do[0, h]
+    np.testing.assert_allclose(dv, expect, atol=1e-12)
+
+
+def test_window_one_and_single_row():
+    k = _rand((1, 2, 8, 4), 4)
+    v = _rand((1, 2, 8, 4), 5)
+    q = _rand((1, 2, 8, 4), 6)
+    o, _ = orc.forward(q, k, v, True, 1)
+    np.testing.assert_allclose(o, v, atol=1e-12)
+    o1, lse1 = orc.forward(q[:, :, :1], k[:, :, :1], v[:, :, :1], True, 0)
+    np.testing.assert_allclose(o1, v[:, :, :1], atol=1e-12)
+
+
+def test_gqa_equals_mha_on_repeated_kv_and_shift_invariance():
+    q = _rand((1, 8, 12, 6), 7)
+    k = _rand((1, 2, 12, 6), 8)
+    v = _rand((1, 2, 12, 6), 9)
+    o, lse = orc.forward(q, k, v, True, 5)
+    o2, lse2 = orc.forward(q, np.repeat(k, 4, axis=1), np.repeat(v, 4, axis=1), True, 5)
+    np.testing.assert_allclose(o, o2, atol=1e-13)
+    np.testing.assert_allclose(lse, lse2, atol=1e-13)
+    # Adding the same vector c to every key shifts each row's scores by q.c: O unchanged.
+    c = _rand((1, 1, 1, 6), 10)
+    o3, _ = orc.forward(q, k + c, v, True, 5)
+    np.testing.assert_allclose(o, o3, atol=1e-12)
+    # Rows are convex combinations of visible values.
+    assert (o <= v.max(axis=2, keepdims=True).repeat(4, axis=1) + 1e-12).all()
+    assert (o >= v.min(axis=2, keepdims=True).repeat(4, axis=1) - 1e-12).all()
+
+
+def test_one_hot_selects_value():
+    n = 6
+    k = np.zeros((1, 1, n, n))
+    k[0, 0] = np.eye(n) * 200.0  # key j is e_j scaled
+    q = np.zeros((1, 1, n, n))
+    q[0, 0, :, 2] = 1.0  # every query points at key 2 (visible from query 2 on)
+    v = _rand((1, 1, n, n), 11)
+    o, _ = orc.forward(q, k, v, False, 0)
+    np.testing.assert_allclose(o[0, 0], np.repeat(v[0, 0, 2:3], n, axis=0), atol=1e-12)
+
+
+@pytest.mark.parametrize("causal,window", [(True, 0), (True, 6), (False, 0)])
+def test_chunked_matches_dense(causal, window):
+    B, Hq, Hkv, N, D = 1, 4, 2, 37, 8
+    q, k, v, do = (_rand(s, 20 + i) for i, s in enumerate([(B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D), (B, Hq, N, D)]))
+    o, lse = orc.forward(q, k, v, causal, window)
+    dq, dk, dv, delta = orc.backward(q, k, v, do, causal, window)
+    tq, tk, tv, tdo = (torch.tensor(x, dtype=torch.float32) for x in (q, k, v, do))
+    o2, lse2 = orc.forward_chunked(tq, tk, tv, causal, window, chunk=8)
+    dq2, dk2, dv2, delta2 = orc.backward_chunked(tq, tk, tv, tdo, causal, window, chunk=8)
+    for a, b in ((o, o2), (lse, lse2), (dq, dq2), (dk, dk2), (dv, dv2), (delta, delta2)):
+        np.testing.assert_allclose(b.numpy(), a, atol=2e-5, rtol=1e-4)
