@@ -19,6 +19,8 @@ LIB_PATH = os.environ.get("GFA_LIBRARY", os.path.join(_HERE, "libgfa.so"))
 
 GFA_DTYPE_FP16 = 0
 GFA_DTYPE_BF16 = 1
+GFA_BWD_DQ = 1
+GFA_BWD_DKV = 2
 
 STATUS_NAMES = {
     0: "GFA_OK",
@@ -67,7 +69,7 @@ class BwdArgs(ctypes.Structure):
         ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32), ("heads_kv", ctypes.c_int32),
         ("seq_len", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("causal", ctypes.c_int32), ("window", ctypes.c_int32), ("scale", ctypes.c_float),
-        ("dtype", ctypes.c_int32), ("q_splits", ctypes.c_int32),
+        ("dtype", ctypes.c_int32), ("q_splits", ctypes.c_int32), ("stages", ctypes.c_int32),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("stream", ctypes.c_void_p),
     ]

@@ -101,18 +101,24 @@ def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bo
     return o, lse
 
 
-def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, q_splits: int = 0):
+def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, q_splits: int = 0,
+              stages: int = 0, out=None):
+    """Run gfa_bwd. ``stages`` selects kernels (0 = all; GFA_BWD_DQ / GFA_BWD_DKV bits);
+    ``out`` = (dq, dk, dv, delta) reuses caller buffers (profiling a single stage)."""
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     do = _prep(do)
     if do.dtype != q.dtype:
         do = do.to(q.dtype)
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
-    dq, dk, dv = (t if not _needs_copy(t) else torch.empty(t.shape, dtype=t.dtype, device=t.device)
-                  for t in (dq, dk, dv))
-    delta = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device)
+    if out is not None:
+        dq, dk, dv, delta = out
+    else:
+        dq = torch.empty_like(q)
+        dk = torch.empty_like(k)
+        dv = torch.empty_like(v)
+        dq, dk, dv = (t if not _needs_copy(t) else torch.empty(t.shape, dtype=t.dtype, device=t.device)
+                      for t in (dq, dk, dv))
+        delta = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device)
     lib = _lib.load()
     ws_bytes = int(lib.gfa_bwd_workspace_size(B, Hq, Hkv, N, D, int(bool(causal)), int(slide_size), int(q_splits)))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
@@ -128,6 +134,7 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
     a.scale = float(scale)
     a.dtype = _DTYPES[q.dtype]
     a.q_splits = int(q_splits)
+    a.stages = int(stages)
     a.workspace = ws.data_ptr() if ws is not None else None
     a.workspace_bytes = ws_bytes
     a.stream = _stream(q.device)

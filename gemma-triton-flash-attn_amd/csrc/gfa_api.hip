@@ -246,8 +246,14 @@ int gfa_bwd(const gfa_bwd_args* a) {
   pq.scale = a->scale;
   pq.scale_log2 = scale_log2;
   pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves);
-  hipError_t err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, bf16, stream);
-  if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dQ launch failed: %s", hipGetErrorString(err));
+  const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
+  if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);
+  hipError_t err = hipSuccess;
+  if (stages & GFA_BWD_DQ) {
+    err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, bf16, stream);
+    if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dQ launch failed: %s", hipGetErrorString(err));
+  }
+  if (!(stages & GFA_BWD_DKV)) return ok();
 
   gfa::BwdDkvParams pk;
   pk.q = pq.q;

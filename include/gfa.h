@@ -48,6 +48,10 @@ typedef enum {
   GFA_ERR_LAUNCH = 4            /* the HIP runtime rejected a kernel launch            */
 } gfa_status;
 
+/* gfa_bwd_args.stages bits */
+#define GFA_BWD_DQ 1  /* delta + dQ kernel */
+#define GFA_BWD_DKV 2 /* dK/dV kernel (+ Q-split reduction) */
+
 /* Element strides (batch, head, row) of one 4-D tensor; the head-dim stride is 1. */
 typedef struct {
   int64_t batch, head, row;
@@ -86,6 +90,8 @@ typedef struct {
   float scale;
   int32_t dtype;
   int32_t q_splits;       /* 0 = registry choice, else 1, 2, 4 or 8 */
+  int32_t stages;         /* 0 = all; else bitwise OR of GFA_BWD_DQ and GFA_BWD_DKV (profiling:
+                             GFA_BWD_DKV alone reads the delta a previous GFA_BWD_DQ wrote) */
   void* workspace;        /* >= gfa_bwd_workspace_size(...) bytes when q_splits > 1 */
   size_t workspace_bytes;
   void* stream;
