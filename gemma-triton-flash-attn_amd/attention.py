@@ -73,6 +73,12 @@ def _norm_window(causal: bool, slide_size: int, n: int) -> int:
     return slide_size
 
 
+def lse_ld(n: int) -> int:
+    """Row length of the LSE / delta buffers: the backward reads whole 32-row groups
+    (GFA_LSE_LD in include/gfa.h)."""
+    return (n + 31) // 32 * 32
+
+
 def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
@@ -84,7 +90,8 @@ def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bo
     o = torch.empty_like(q)
     if _needs_copy(o):
         o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    lse = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device) if store_lse else None
+    ld = lse_ld(N)
+    lse = torch.empty((B, Hq, ld), dtype=torch.float32, device=q.device) if store_lse else None
     a = _lib.FwdArgs()
     a.q, a.k, a.v, a.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
     a.lse = lse.data_ptr() if lse is not None else None
@@ -95,10 +102,11 @@ def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bo
     a.scale = float(scale)
     a.dtype = _DTYPES[q.dtype]
     a.block_kv = int(block_kv)
+    a.lse_ld = ld
     a.stream = _stream(q.device)
     with torch.cuda.device(q.device):
         _lib.check(_lib.load().gfa_fwd(ctypes.byref(a)))
-    return o, lse
+    return o, lse  # lse is (B, Hq, lse_ld(N)); rows >= N are padding
 
 
 def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, q_splits: int = 0,
@@ -118,7 +126,7 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
         dv = torch.empty_like(v)
         dq, dk, dv = (t if not _needs_copy(t) else torch.empty(t.shape, dtype=t.dtype, device=t.device)
                       for t in (dq, dk, dv))
-        delta = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device)
+        delta = torch.empty((B, Hq, lse_ld(N)), dtype=torch.float32, device=q.device)
     lib = _lib.load()
     ws_bytes = int(lib.gfa_bwd_workspace_size(B, Hq, Hkv, N, D, int(bool(causal)), int(slide_size), int(q_splits)))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
@@ -134,6 +142,7 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
     a.scale = float(scale)
     a.dtype = _DTYPES[q.dtype]
     a.q_splits = int(q_splits)
+    a.lse_ld = lse.shape[-1]
     a.stages = int(stages)
     a.workspace = ws.data_ptr() if ws is not None else None
     a.workspace_bytes = ws_bytes

@@ -172,6 +172,10 @@ int gfa_fwd(const gfa_fwd_args* a) {
   p.window = (a->causal && a->window > 0 && a->window < a->seq_len) ? a->window : 0;
   p.scale_log2 = a->scale * 1.4426950408889634f;
   p.store_lse = a->lse != nullptr;
+  p.lse_ld = a->lse_ld;
+  if (p.store_lse && (a->lse_ld < GFA_LSE_LD(a->seq_len) || !aligned16(a->lse) || (a->lse_ld & 3)))
+    return fail(GFA_ERR_INVALID_ARGUMENT, "lse_ld=%d must be >= %d (multiple of 4, 16-byte aligned lse)", a->lse_ld,
+                GFA_LSE_LD(a->seq_len));
   p.g = make_qgrid(p.B, p.Hkv, p.R, p.N, nw);
   if (p.g.nblocks <= 0) return fail(GFA_ERR_INVALID_ARGUMENT, "empty grid");
   const hipError_t err = gfa::launch_fwd(p, a->head_dim, bkv, nw, a->dtype == GFA_DTYPE_BF16,
@@ -205,6 +209,9 @@ int gfa_bwd(const gfa_bwd_args* a) {
   if ((rc = check_view("dk", a->dk, a->dk_strides, true))) return rc;
   if ((rc = check_view("dv", a->dv, a->dv_strides, true))) return rc;
   if (a->lse == nullptr || a->delta == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "lse and delta are required");
+  if (a->lse_ld < GFA_LSE_LD(a->seq_len) || (a->lse_ld & 3) || !aligned16(a->lse) || !aligned16(a->delta))
+    return fail(GFA_ERR_INVALID_ARGUMENT, "lse_ld=%d must be >= %d (multiple of 4, 16-byte aligned lse/delta)",
+                a->lse_ld, GFA_LSE_LD(a->seq_len));
   if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
   const Entry* e = lookup(a->head_dim);
   const int qs = a->q_splits > 0 ? a->q_splits : pick_q_splits(a->batch, a->heads_kv, a->seq_len, e->dkv_waves);
@@ -245,6 +252,7 @@ int gfa_bwd(const gfa_bwd_args* a) {
   pq.window = window;
   pq.scale = a->scale;
   pq.scale_log2 = scale_log2;
+  pq.lse_ld = a->lse_ld;
   pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves);
   const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
   if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);
@@ -281,6 +289,7 @@ int gfa_bwd(const gfa_bwd_args* a) {
   pk.scale = a->scale;
   pk.scale_log2 = scale_log2;
   pk.q_splits = qs;
+  pk.lse_ld = a->lse_ld;
   const int keys_per_wg = 32 * (e->dkv_waves / 2);
   pk.n_kb = (pk.N + keys_per_wg - 1) / keys_per_wg;
   pk.nblocks = pk.n_kb * pk.B * pk.Hkv * qs;

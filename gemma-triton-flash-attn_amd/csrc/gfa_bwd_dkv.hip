@@ -82,15 +82,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
   const int it_lo = min(total, split * chunk);
   const int it_hi = min(total, it_lo + chunk);
 
-  // Queries any key of this pair serves [vis_lo, vis_hi); queries every key serves [all_lo, all_hi).
-  int vis_lo = 0, vis_hi = p.N, all_lo = 0, all_hi = p.N;
+  // Queries every key of this pair serves: [all_lo, all_hi).
+  int all_lo = 0, all_hi = p.N;
   if (p.causal) {
-    vis_lo = k0;
     all_lo = k_last;
-    if (swa) {
-      vis_hi = min(p.N, k_last + p.window);   // q - key < window
-      all_hi = min(p.N, k0 + p.window);
-    }
+    if (swa) all_hi = min(p.N, k0 + p.window);  // q - key < window for the first key
   }
   const bool pair_full = k_last < p.N;
 
@@ -103,6 +99,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
     for (int kk = 0; kk < KTH; ++kk) {
       kf[kk] = *reinterpret_cast<const i16x8*>(kr + 16 * kk);
       vf[kk] = *reinterpret_cast<const i16x8*>(vr + 16 * kk);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KTH; ++kk) {
+      pin_agpr(kf[kk]);
+      pin_agpr(vf[kk]);
     }
   }
 
@@ -150,36 +151,37 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
   for (int it = it_lo; it < it_hi; ++it) {
     const int cur = (it - it_lo) & 1;
     barrier_tile();
-    if (it + 1 < it_hi) {
+    {
+      // Prefetch the next tile; the last iteration re-fetches its own tile into the idle
+      // buffer (never read) so the loop body stays branch-free.
+      const int itn = min(it + 1, it_hi - 1);
       int qs1;
-      const uint16_t* qb = tile_src(it + 1, p.q, p.qv, qs1);
-      const uint16_t* db = tile_src(it + 1, p.dout, p.dov, qs1);
+      const uint16_t* qb = tile_src(itn, p.q, p.qv, qs1);
+      const uint16_t* db = tile_src(itn, p.dout, p.dov, qs1);
       load_tile_async<D, BQ, NW>(qb, p.qv.sn, qs1, p.N, smem + (cur ^ 1) * TILE, wave, lane);
       load_tile_async<D, BQ, NW>(db, p.dov.sn, qs1, p.N, smem + (2 + (cur ^ 1)) * TILE, wave, lane);
     }
     const int head = kvh * p.R + it / nqt;
     const int q0 = (qt_lo + it % nqt) * BQ;
-    const bool live = active && q0 < vis_hi && q0 + BQ > vis_lo;
     const char GFA_LDS* qt = smem + cur * TILE;
     const char GFA_LDS* dt = smem + (2 + cur) * TILE;
 
+    // Every tile runs the same straight-line code (no per-pair skip): a tile a pair cannot
+    // see is fully masked below. Branch-free bodies keep the dK/dV accumulators resident.
     f32x16 s[SB], dp[SB];
-    if (live) {
 #pragma unroll
-      for (int sb = 0; sb < SB; ++sb) {
-        s[sb] = mma_chain_lds<IS_BF16, KTH, 4>(qt, roff, sb * 32 * (2 * D), kf);
-        dp[sb] = mma_chain_lds<IS_BF16, KTH, 4>(dt, roff, sb * 32 * (2 * D), vf);
+    for (int sb = 0; sb < SB; ++sb) {
+      s[sb] = mma_chain_lds<IS_BF16, KTH, 4>(qt, roff, sb * 32 * (2 * D), kf);
+      dp[sb] = mma_chain_lds<IS_BF16, KTH, 4>(dt, roff, sb * 32 * (2 * D), vf);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x4 vs = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
-          const f32x4 vd = {dp[sb][4 * j], dp[sb][4 * j + 1], dp[sb][4 * j + 2], dp[sb][4 * j + 3]};
-          *reinterpret_cast<f32x4 GFA_LDS*>(xmine + (sb * 4 + j) * 1024) = vs;
-          *reinterpret_cast<f32x4 GFA_LDS*>(xmine + XHALF + (sb * 4 + j) * 1024) = vd;
-        }
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 vs = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
+        const f32x4 vd = {dp[sb][4 * j], dp[sb][4 * j + 1], dp[sb][4 * j + 2], dp[sb][4 * j + 3]};
+        *reinterpret_cast<f32x4 GFA_LDS*>(xmine + (sb * 4 + j) * 1024) = vs;
+        *reinterpret_cast<f32x4 GFA_LDS*>(xmine + XHALF + (sb * 4 + j) * 1024) = vd;
       }
     }
     barrier_lds();
-    if (!live) continue;
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
@@ -195,43 +197,47 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
     }
 
     // ---- P and dS on the key lanes; rows (queries) are per-register ----
-    const bool need_mask = !(pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
-    const float* lse_row = p.lse + ((int64_t)b * p.Hq + head) * p.N;
-    const float* del_row = p.delta + ((int64_t)b * p.Hq + head) * p.N;
-    i16x8 pb[BQ / 16], dsb[BQ / 16];
+    // LSE / delta rows are padded to a multiple of 32, so whole 4-row groups are readable.
+    const float* lse_row = p.lse + ((int64_t)b * p.Hq + head) * p.lse_ld;
+    const float* del_row = p.delta + ((int64_t)b * p.Hq + head) * p.lse_ld;
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int qq = q0 + sb * 32 + 8 * g + 4 * h;  // rows qq .. qq+3 of this lane
-        f32x4 lse4, del4;
-        if (qq + 3 < p.N) {
-          lse4 = *reinterpret_cast<const f32x4*>(lse_row + qq);
-          del4 = *reinterpret_cast<const f32x4*>(del_row + qq);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int qe = min(qq + e, p.N - 1);
-            lse4[e] = lse_row[qe];
-            del4[e] = del_row[qe];
-          }
-        }
+        const f32x4 lse4 = *reinterpret_cast<const f32x4*>(lse_row + qq);
+        const f32x4 del4 = *reinterpret_cast<const f32x4*>(del_row + qq);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
-          float pv = fast_exp2(s[sb][r] * p.scale_log2 - lse4[e] * kLog2e);
-          float ds = pv * (dp[sb][r] - del4[e]);
-          if (need_mask) {
-            const int qi = qq + e;
-            bool ok = key < p.N && qi < p.N;
-            if (p.causal) ok = ok && key <= qi;
-            if (swa) ok = ok && (qi - key) < p.window;
-            pv = ok ? pv : 0.f;
-            ds = ok ? ds : 0.f;
-          }
-          pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
-          dsb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(ds);
+          const float pv = fast_exp2(s[sb][r] * p.scale_log2 - lse4[e] * kLog2e);
+          s[sb][r] = pv;
+          dp[sb][r] = pv * (dp[sb][r] - del4[e]);
         }
+      }
+    }
+    const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
+    if (need_mask) {
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qi = q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          bool ok = key < p.N && qi < p.N;
+          if (p.causal) ok = ok && key <= qi;
+          if (swa) ok = ok && (qi - key) < p.window;
+          s[sb][r] = ok ? s[sb][r] : 0.f;
+          dp[sb][r] = ok ? dp[sb][r] : 0.f;
+        }
+      }
+    }
+    i16x8 pb[BQ / 16], dsb[BQ / 16];
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(s[sb][r]);
+        dsb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(dp[sb][r]);
       }
     }
 

@@ -68,14 +68,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 
   const bool active = q0 < p.N;
   const int q_last = q0 + 31;
-  int vis_lo = 0, vis_hi = p.N, all_lo = 0, all_hi = p.N;
+  int all_lo = 0, all_hi = p.N;
   if (p.causal) {
-    vis_hi = min(p.N, q_last + 1);
     all_hi = min(p.N, q0 + 1);
-    if (swa) {
-      vis_lo = max(0, q0 - p.window + 1);
-      all_lo = q_last - p.window + 1;
-    }
+    if (swa) all_lo = q_last - p.window + 1;
   }
 
   const int q = q0 + l32;
@@ -96,13 +92,18 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       for (int e = 0; e < 8; ++e) dpart += from16<IS_BF16>(df[kk][e]) * from16<IS_BF16>(of[e]);
     }
   }
+#pragma unroll
+  for (int kk = 0; kk < KTH; ++kk) {
+    pin_agpr(qf[kk]);
+    pin_agpr(df[kk]);
+  }
   dpart += __shfl_xor(dpart, 32);
   // Pair exchange of the two head-dim halves of delta (through the exchange area).
   *reinterpret_cast<float GFA_LDS*>(xch + wave * XCH + lane * 4) = dpart;
   barrier_lds();
   const float delta = dpart + *reinterpret_cast<const float GFA_LDS*>(xch + (wave ^ 1) * XCH + lane * 4);
-  if (active && q < p.N && dh == 0 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.N + q] = delta;
-  const float lse_log2 = p.lse[((int64_t)b * p.Hq + head) * p.N + qrow] * kLog2e;
+  if (active && q < p.N && dh == 0 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.lse_ld + q] = delta;
+  const float lse_log2 = p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + qrow] * kLog2e;
 
   f32x16 acc[DBH];
 #pragma unroll
@@ -139,17 +140,21 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   for (int t = t_lo; t < t_hi; ++t) {
     const int cur = (t - t_lo) & 1;
     barrier_tile();
-    if (t + 1 < t_hi) {
-      load_tile_async<D, BKV, NW>(kbase, p.kv.sn, (t + 1) * BKV, p.N, smem + (cur ^ 1) * TILE, wave, lane);
-      load_tile_async<D, BKV, NW>(vbase, p.vv.sn, (t + 1) * BKV, p.N, smem + (2 + (cur ^ 1)) * TILE, wave, lane);
+    {
+      // Prefetch the next tile; the last iteration re-fetches its own tile into the idle
+      // buffer (never read) so the loop body stays branch-free.
+      const int tn = min(t + 1, t_hi - 1);
+      load_tile_async<D, BKV, NW>(kbase, p.kv.sn, tn * BKV, p.N, smem + (cur ^ 1) * TILE, wave, lane);
+      load_tile_async<D, BKV, NW>(vbase, p.vv.sn, tn * BKV, p.N, smem + (2 + (cur ^ 1)) * TILE, wave, lane);
     }
     const int k0 = t * BKV;
-    const bool live = active && k0 < vis_hi && k0 + BKV > vis_lo;
     const char GFA_LDS* kt = smem + cur * TILE;
     const char GFA_LDS* vt = smem + (2 + cur) * TILE;
 
     f32x16 s[SB], dp[SB];
-    if (live) {
+    {
+      // No per-pair skip: a tile this pair cannot see is fully masked below, and the
+      // straight-line body keeps the accumulators resident in registers.
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
         s[sb] = mma_chain_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
@@ -164,7 +169,6 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       }
     }
     barrier_lds();
-    if (!live) continue;
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       }
     }
 
-    const bool need_mask = !(k0 + BKV <= all_hi && k0 >= all_lo);
+    const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
     i16x8 dsb[BKV / 16];
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {

@@ -61,6 +61,11 @@ __device__ __forceinline__ float from16(short x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Keep a kernel-lifetime MFMA operand fragment in AGPRs. MFMA reads A/B operands from
+// AGPRs directly; left alone, the allocator keeps such fragments in the 256 arch VGPRs
+// and spills once the fp32 accumulators fill the AGPR file.
+__device__ __forceinline__ void pin_agpr(i16x8& x) { asm volatile("" : "+a"(x)); }
+
 // XOR swizzle of the 16-byte chunk index inside one LDS tile row. It makes
 //  * ds_read_b128 of one chunk column across 16 consecutive rows hit 16 distinct
 //    4-bank groups, and
@@ -116,25 +121,17 @@ __device__ __forceinline__ void load_tile_async(const uint16_t* gbase, int64_t r
   static_assert(BKV * CPR % (64 * NW) == 0, "tile must split evenly over the waves");
   const int lrow = lane / CPR;
   const int lc = lane % CPR;
-  if (row0 + BKV <= n_rows) {
-    const int lrow_off = lrow * (int)row_stride * 2;
+  const int stride_b = (int)row_stride * 2;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int grp = i * NW + wave;
-      const int row = grp * RPI + lrow;
-      const char* rbase = reinterpret_cast<const char*>(gbase + (int64_t)(row0 + grp * RPI) * row_stride);
-      const unsigned voff = (unsigned)(lrow_off + ((lc ^ swz(row)) << 4));
-      dma16(rbase + voff, tile + grp * 1024);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int grp = i * NW + wave;
-      const int row = grp * RPI + lrow;
-      const int grow = min(row0 + row, n_rows - 1);
-      const uint16_t* src = gbase + (int64_t)grow * row_stride + ((lc ^ swz(row)) << 3);
-      dma16(src, tile + grp * 1024);
-    }
+  for (int i = 0; i < NI; ++i) {
+    const int grp = i * NW + wave;
+    // Rows past the end re-read the last row (their scores are masked); the clamp is
+    // branch-free: scalar group base, per-lane row offset min(lrow, last - base).
+    const int srow = min(row0 + grp * RPI, n_rows - 1);
+    const int lr = min(lrow, n_rows - 1 - srow);
+    const char* rbase = reinterpret_cast<const char*>(gbase + (int64_t)srow * row_stride);
+    const unsigned voff = (unsigned)(lr * stride_b + ((lc ^ swz(grp * RPI + lrow)) << 4));
+    dma16(rbase + voff, tile + grp * 1024);
   }
 }
 

@@ -77,17 +77,13 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(const FwdParams p) {
   const int t_lo = k_lo / BKV;
   const int t_hi = (k_hi + BKV - 1) / BKV;
 
-  // Keys any query of this pair may see [vis_lo, vis_hi), keys all of them see [all_lo, all_hi).
+  // Keys every query of this pair sees: [all_lo, all_hi).
   const bool active = q0 < p.N;
   const int q_last = q0 + 31;
-  int vis_lo = 0, vis_hi = p.N, all_lo = 0, all_hi = p.N;
+  int all_lo = 0, all_hi = p.N;
   if (p.causal) {
-    vis_hi = min(p.N, q_last + 1);
     all_hi = min(p.N, q0 + 1);
-    if (swa) {
-      vis_lo = max(0, q0 - p.window + 1);
-      all_lo = q_last - p.window + 1;
-    }
+    if (swa) all_lo = q_last - p.window + 1;
   }
 
   // ---- Q half fragments (B operand of S^T = K Q^T), resident for the whole kernel ----
@@ -137,18 +133,22 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(const FwdParams p) {
   for (int t = t_lo; t < t_hi; ++t) {
     const int cur = (t - t_lo) & 1;
     barrier_tile();  // tile t landed; every wave is done with tile t-1 and its exchange slot
-    if (t + 1 < t_hi) {
-      load_tile_async<D, BKV, NW>(kbase, p.kv.sn, (t + 1) * BKV, p.N, smem + (cur ^ 1) * TILE, wave, lane);
-      load_tile_async<D, BKV, NW>(vbase, p.vv.sn, (t + 1) * BKV, p.N, smem + (2 + (cur ^ 1)) * TILE, wave, lane);
+    {
+      // Prefetch the next tile; the last iteration re-fetches its own tile into the idle
+      // buffer (never read) so the loop body stays branch-free.
+      const int tn = min(t + 1, t_hi - 1);
+      load_tile_async<D, BKV, NW>(kbase, p.kv.sn, tn * BKV, p.N, smem + (cur ^ 1) * TILE, wave, lane);
+      load_tile_async<D, BKV, NW>(vbase, p.vv.sn, tn * BKV, p.N, smem + (2 + (cur ^ 1)) * TILE, wave, lane);
     }
     const int k0 = t * BKV;
-    const bool live = active && k0 < vis_hi && k0 + BKV > vis_lo;  // pair-uniform
     const char GFA_LDS* kt = smem + cur * TILE;
     const char GFA_LDS* vt = smem + (2 + cur) * TILE;
 
     // ---- partial S^T = K[:, half] Q[:, half]^T, published to the partner ----
     f32x16 s[SB];
-    if (live) {
+    {
+      // No per-pair skip: a tile this pair cannot see is fully masked below, and the
+      // straight-line body keeps the accumulators resident in registers.
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
         s[sb] = mma_chain_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
@@ -160,7 +160,6 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(const FwdParams p) {
       }
     }
     barrier_lds();  // partials visible
-    if (!live) continue;
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
@@ -173,7 +172,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(const FwdParams p) {
     }
 
     // ---- online softmax (lane = query column) ----
-    const bool need_mask = !(k0 + BKV <= all_hi && k0 >= all_lo);
+    const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
     if (need_mask) {
       const int q = q0 + l32;
 #pragma unroll
@@ -248,7 +247,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(const FwdParams p) {
       }
     }
     if (p.store_lse && h == 0 && dh == 0) {
-      p.lse[((int64_t)b * p.Hq + head) * p.N + q] = (m_run + __log2f(l_tot)) * kLn2;
+      p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + q] = (m_run + __log2f(l_tot)) * kLn2;
     }
   }
 }

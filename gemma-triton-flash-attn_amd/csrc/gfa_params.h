@@ -26,13 +26,14 @@ struct FwdParams {
   const uint16_t* k;
   const uint16_t* v;
   uint16_t* o;
-  float* lse;  // (B, Hq, N) contiguous, natural log; may be null when store_lse == 0
+  float* lse;  // (B, Hq, lse_ld), natural log; may be null when store_lse == 0
   RowView qv, kv, vv, ov;
   int B, Hq, Hkv, N, R;
   int causal;
   int window;        // 0 = no sliding window; only honoured when causal
   float scale_log2;  // softmax scale * log2(e)
   int store_lse;
+  int lse_ld;
   QGrid g;
 };
 
@@ -42,14 +43,15 @@ struct BwdDqParams {
   const uint16_t* v;
   const uint16_t* o;
   const uint16_t* dout;
-  const float* lse;  // (B, Hq, N)
-  float* delta;      // (B, Hq, N), written: rowsum(dO * O)
+  const float* lse;  // (B, Hq, lse_ld)
+  float* delta;      // (B, Hq, lse_ld), written: rowsum(dO * O)
   uint16_t* dq;
   RowView qv, kv, vv, ov, dov, dqv;
   int B, Hq, Hkv, N, R;
   int causal, window;
   float scale;       // softmax scale (applied to dQ at the end)
   float scale_log2;  // scale * log2(e)
+  int lse_ld;
   QGrid g;
 };
 
@@ -58,8 +60,8 @@ struct BwdDkvParams {
   const uint16_t* k;
   const uint16_t* v;
   const uint16_t* dout;
-  const float* lse;
-  const float* delta;
+  const float* lse;    // (B, Hq, lse_ld), rows padded to a multiple of 32
+  const float* delta;  // same layout
   uint16_t* dk;      // written directly when q_splits == 1
   uint16_t* dv;
   float* part;       // fp32 partials [q_splits][2][B][Hkv][N][D] when q_splits > 1
@@ -68,6 +70,7 @@ struct BwdDkvParams {
   int causal, window;
   float scale, scale_log2;
   int q_splits;
+  int lse_ld;
   int n_kb;          // number of key blocks (each WKV keys wide)
   int nblocks;
 };

@@ -7,8 +7,10 @@
  *
  * Tensor layout: q/o/do/dq are (B, Hq, N, D); k/v/dk/dv are (B, Hkv, N, D); every
  * tensor is addressed through its own (batch, head, row) element strides and must have
- * a unit-stride head dimension and 16-byte aligned rows. lse/delta are contiguous
- * (B, Hq, N) float32. Query head h reads KV head h / (Hq / Hkv) (contiguous groups).
+ * a unit-stride head dimension and 16-byte aligned rows. lse/delta are float32
+ * (B, Hq, lse_ld) with lse_ld >= GFA_LSE_LD(N): the backward kernels read whole 32-row
+ * groups, so rows N..lse_ld-1 must exist (their values are never used).
+ * Query head h reads KV head h / (Hq / Hkv) (contiguous groups).
  *
  * The entry points replace the reference's Triton launch sites (file:line in
  * /root/reference, zzhhjjj/gemma-triton-flash-attn):
@@ -48,6 +50,9 @@ typedef enum {
   GFA_ERR_LAUNCH = 4            /* the HIP runtime rejected a kernel launch            */
 } gfa_status;
 
+/* Smallest legal lse_ld for a sequence length. */
+#define GFA_LSE_LD(seq_len) ((((seq_len) + 31) / 32) * 32)
+
 /* gfa_bwd_args.stages bits */
 #define GFA_BWD_DQ 1  /* delta + dQ kernel */
 #define GFA_BWD_DKV 2 /* dK/dV kernel (+ Q-split reduction) */
@@ -62,7 +67,7 @@ typedef struct {
   const void* k;
   const void* v;
   void* o;
-  float* lse; /* (B, Hq, N) natural-log logsumexp; NULL = inference (not stored) */
+  float* lse; /* (B, Hq, lse_ld) natural-log logsumexp; NULL = inference (not stored) */
   gfa_strides q_strides, k_strides, v_strides, o_strides;
   int32_t batch, heads_q, heads_kv, seq_len, head_dim;
   int32_t causal;      /* 0 / 1 */
@@ -70,6 +75,7 @@ typedef struct {
   float scale;         /* softmax scale; the reference uses 1/sqrt(head_dim) */
   int32_t dtype;       /* gfa_dtype, shared by q/k/v/o */
   int32_t block_kv;    /* 0 = registry default, else a built tile width */
+  int32_t lse_ld;      /* row length of lse (>= GFA_LSE_LD(seq_len)); ignored when lse == NULL */
   void* stream;        /* hipStream_t */
 } gfa_fwd_args;
 
@@ -79,8 +85,8 @@ typedef struct {
   const void* v;
   const void* o;
   const void* dout;
-  const float* lse; /* from gfa_fwd */
-  float* delta;     /* (B, Hq, N) scratch written by the dQ kernel: rowsum(dO * O) */
+  const float* lse; /* from gfa_fwd, (B, Hq, lse_ld) */
+  float* delta;     /* (B, Hq, lse_ld) scratch written by the dQ kernel: rowsum(dO * O) */
   void* dq;
   void* dk;
   void* dv;
@@ -90,6 +96,7 @@ typedef struct {
   float scale;
   int32_t dtype;
   int32_t q_splits;       /* 0 = registry choice, else 1, 2, 4 or 8 */
+  int32_t lse_ld;         /* row length of lse and delta (>= GFA_LSE_LD(seq_len)) */
   int32_t stages;         /* 0 = all; else bitwise OR of GFA_BWD_DQ and GFA_BWD_DKV (profiling:
                              GFA_BWD_DKV alone reads the delta a previous GFA_BWD_DQ wrote) */
   void* workspace;        /* >= gfa_bwd_workspace_size(...) bytes when q_splits > 1 */
