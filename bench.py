@@ -160,6 +160,10 @@ def main(argv=None):
     ap.add_argument("--all", action="store_true", help="also time BASELINE configs 2 and 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernels", action="store_true", help="skip per-kernel timing")
+    ap.add_argument("--workloads", default="d512_causal_gqa8_n16k,d256_swa1024_gqa2_n16k",
+                    help="comma list of workloads to time (the first one must be the headline)")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="also run a plain device copy of this many MiB (rocprof FETCH/WRITE_SIZE calibration)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this engine is a single-GPU build; --gpus {args.gpus} is not supported "
@@ -173,11 +177,27 @@ def main(argv=None):
         return 1
     device = torch.device("cuda:0")
     head = "d512_causal_gqa8_n16k"
-    results = {head: bench_workload(head, WORKLOADS[head], args.steps, args.warmup, device,
-                                    kernels=not args.no_kernels)}
-    swa = "d256_swa1024_gqa2_n16k"
-    results[swa] = bench_workload(swa, WORKLOADS[swa], max(args.steps, 10), args.warmup, device,
-                                  kernels=not args.no_kernels)
+    names = [n for n in args.workloads.split(",") if n]
+    for n in names:
+        if n not in WORKLOADS:
+            print(f"bench.py: unknown workload {n}; choose from {sorted(WORKLOADS)}", file=sys.stderr)
+            return 2
+    results = {}
+    for n in names:
+        steps = args.steps if n != "d256_swa1024_gqa2_n16k" else max(args.steps, 10)
+        results[n] = bench_workload(n, WORKLOADS[n], steps, args.warmup, device, kernels=not args.no_kernels)
+    if args.copy_calib_mib:
+        nbytes = args.copy_calib_mib << 20
+        src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=device).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] copy calibration: 3 x {args.copy_calib_mib} MiB device copies", file=sys.stderr, flush=True)
+        del src, dst
+    if head not in results:
+        print(json.dumps({"metric": METRIC, "workloads": results}), flush=True)
+        return 0
     if args.all:
         for name in ("c2_d512_causal_gqa8_n8k", "c4_d512_causal_gqa8_n32k"):
             results[name] = bench_workload(name, WORKLOADS[name], args.steps, args.warmup, device, kernels=False)

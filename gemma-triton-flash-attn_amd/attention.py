@@ -51,11 +51,11 @@ def _check_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise TypeError(f"dtype {q.dtype} not supported (fp16 / bf16)")
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise TypeError("q, k, v must share one dtype")
+    lookup(D)
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise ValueError("q, k, v must be GPU tensors (the engine has no CPU path)")
     if k.device != q.device or v.device != q.device:
         raise ValueError("q, k, v must be on the same device")
-    lookup(D)
     if N == 0 or B == 0:
         raise ValueError("empty sequence or batch")
 

@@ -53,7 +53,7 @@ const Entry* lookup(int d) {
 }
 
 bool fwd_built(int d, int bkv, int nw) {
-  return (d == 512 && bkv == 32 && (nw == 4 || nw == 8)) || (d == 256 && (bkv == 32 || bkv == 64) && nw == 4);
+  return nw == 4 && ((d == 512 && bkv == 32) || (d == 256 && (bkv == 32 || bkv == 64)));
 }
 
 int largest_pow2_divisor_le(int r, int cap) {
@@ -62,9 +62,10 @@ int largest_pow2_divisor_le(int r, int cap) {
   return x;
 }
 
-gfa::QGrid make_qgrid(int B, int Hkv, int R, int N, int nw) {
+// units = 32-row query blocks per workgroup: one per wave in the forward kernel, one per
+// wave pair in the dQ kernel.
+gfa::QGrid make_qgrid(int B, int Hkv, int R, int N, int nu) {
   gfa::QGrid g;
-  const int nu = nw / 2;
   g.hpw = largest_pow2_divisor_le(R, nu);
   g.qbw = nu / g.hpw;
   g.n_hg = R / g.hpw;
@@ -126,7 +127,7 @@ int gfa_config(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len
   out->fwd_block_q = 32 * g.qbw;
   out->fwd_block_kv = e->fwd_bkv;
   out->fwd_waves = e->fwd_waves;
-  const gfa::QGrid gq = make_qgrid(batch, heads_kv, heads_q / heads_kv, seq_len, e->dq_waves);
+  const gfa::QGrid gq = make_qgrid(batch, heads_kv, heads_q / heads_kv, seq_len, e->dq_waves / 2);
   out->dq_block_q = 32 * gq.qbw;
   out->dq_block_kv = e->dq_bkv;
   out->dq_waves = e->dq_waves;
@@ -213,6 +214,8 @@ int gfa_bwd(const gfa_bwd_args* a) {
     return fail(GFA_ERR_INVALID_ARGUMENT, "lse_ld=%d must be >= %d (multiple of 4, 16-byte aligned lse/delta)",
                 a->lse_ld, GFA_LSE_LD(a->seq_len));
   if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
+  const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
+  if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);
   const Entry* e = lookup(a->head_dim);
   const int qs = a->q_splits > 0 ? a->q_splits : pick_q_splits(a->batch, a->heads_kv, a->seq_len, e->dkv_waves);
   if (qs != 1 && qs != 2 && qs != 4 && qs != 8) return fail(GFA_ERR_INVALID_ARGUMENT, "q_splits=%d not in {1,2,4,8}", qs);
@@ -253,9 +256,7 @@ int gfa_bwd(const gfa_bwd_args* a) {
   pq.scale = a->scale;
   pq.scale_log2 = scale_log2;
   pq.lse_ld = a->lse_ld;
-  pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves);
-  const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
-  if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);
+  pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves / 2);
   hipError_t err = hipSuccess;
   if (stages & GFA_BWD_DQ) {
     err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, bf16, stream);

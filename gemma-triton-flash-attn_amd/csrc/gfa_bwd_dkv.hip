@@ -133,6 +133,9 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
   char GFA_LDS* xmine = xch + wave * XCH + lane * 16;
   const char GFA_LDS* xpart = xch + (wave ^ 1) * XCH + lane * 16;
 
+  TileLoader<D, BQ, NW> qload, dload;
+  qload.init(p.q, p.qv.sn, p.N, wave, lane);
+  dload.init(p.dout, p.dov.sn, p.N, wave, lane);
   auto tile_src = [&](int it, const uint16_t* base, const RowView& v, int& q_start) {
     const int r = it / nqt;
     const int qt = qt_lo + it % nqt;
@@ -144,8 +147,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
     int qs0;
     const uint16_t* qb = tile_src(it_lo, p.q, p.qv, qs0);
     const uint16_t* db = tile_src(it_lo, p.dout, p.dov, qs0);
-    load_tile_async<D, BQ, NW>(qb, p.qv.sn, qs0, p.N, smem, wave, lane);
-    load_tile_async<D, BQ, NW>(db, p.dov.sn, qs0, p.N, smem + 2 * TILE, wave, lane);
+    qload.rebase(qb, p.qv.sn, p.N);
+    dload.rebase(db, p.dov.sn, p.N);
+    qload.load(qs0, smem);
+    dload.load(qs0, smem + 2 * TILE);
   }
 
   for (int it = it_lo; it < it_hi; ++it) {
@@ -158,8 +163,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
       int qs1;
       const uint16_t* qb = tile_src(itn, p.q, p.qv, qs1);
       const uint16_t* db = tile_src(itn, p.dout, p.dov, qs1);
-      load_tile_async<D, BQ, NW>(qb, p.qv.sn, qs1, p.N, smem + (cur ^ 1) * TILE, wave, lane);
-      load_tile_async<D, BQ, NW>(db, p.dov.sn, qs1, p.N, smem + (2 + (cur ^ 1)) * TILE, wave, lane);
+      qload.rebase(qb, p.qv.sn, p.N);
+      dload.rebase(db, p.dov.sn, p.N);
+      qload.load(qs1, smem + (cur ^ 1) * TILE);
+      dload.load(qs1, smem + (2 + (cur ^ 1)) * TILE);
     }
     const int head = kvh * p.R + it / nqt;
     const int q0 = (qt_lo + it % nqt) * BQ;
@@ -223,9 +230,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int qi = q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          bool ok = key < p.N && qi < p.N;
-          if (p.causal) ok = ok && key <= qi;
-          if (swa) ok = ok && (qi - key) < p.window;
+          const bool ok = visible(qi, key, p.N, p.causal, p.window);
           s[sb][r] = ok ? s[sb][r] : 0.f;
           dp[sb][r] = ok ? dp[sb][r] : 0.f;
         }
@@ -334,6 +339,14 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const BwdDkvParams p, i
   for (int e = 0; e < 8; ++e) o[e] = to16<IS_BF16>(acc[e]);
   *reinterpret_cast<i16x8*>(dst) = o;
 }
+
+// Explicit instantiations of every built variant (device code and host launch stubs).
+template __global__ void bwd_dkv_kernel<512, 32, true, 4>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<512, 32, false, 4>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<256, 32, true, 4>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<256, 32, false, 4>(const BwdDkvParams);
+template __global__ void dkv_reduce_kernel<true>(const BwdDkvParams, int);
+template __global__ void dkv_reduce_kernel<false>(const BwdDkvParams, int);
 
 template <int D, int BQ, bool IS_BF16, int NW>
 static hipError_t launch_dkv_t(const BwdDkvParams& p, hipStream_t stream) {

@@ -130,11 +130,14 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 
   const uint16_t* kbase = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh;
   const uint16_t* vbase = p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh;
+  TileLoader<D, BKV, NW> kload, vload;
+  kload.init(kbase, p.kv.sn, p.N, wave, lane);
+  vload.init(vbase, p.vv.sn, p.N, wave, lane);
 
   barrier_lds();  // everyone has read the delta exchange before it is overwritten
   if (t_lo < t_hi) {
-    load_tile_async<D, BKV, NW>(kbase, p.kv.sn, t_lo * BKV, p.N, smem, wave, lane);
-    load_tile_async<D, BKV, NW>(vbase, p.vv.sn, t_lo * BKV, p.N, smem + 2 * TILE, wave, lane);
+    kload.load(t_lo * BKV, smem);
+    vload.load(t_lo * BKV, smem + 2 * TILE);
   }
 
   for (int t = t_lo; t < t_hi; ++t) {
@@ -144,8 +147,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       // Prefetch the next tile; the last iteration re-fetches its own tile into the idle
       // buffer (never read) so the loop body stays branch-free.
       const int tn = min(t + 1, t_hi - 1);
-      load_tile_async<D, BKV, NW>(kbase, p.kv.sn, tn * BKV, p.N, smem + (cur ^ 1) * TILE, wave, lane);
-      load_tile_async<D, BKV, NW>(vbase, p.vv.sn, tn * BKV, p.N, smem + (2 + (cur ^ 1)) * TILE, wave, lane);
+      kload.load(tn * BKV, smem + (cur ^ 1) * TILE);
+      vload.load(tn * BKV, smem + (2 + (cur ^ 1)) * TILE);
     }
     const int k0 = t * BKV;
     const char GFA_LDS* kt = smem + cur * TILE;
@@ -193,9 +196,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
         float ds = pv * (dp[sb][r] - delta);
         if (need_mask) {
           const int key = k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          bool ok = key < p.N;
-          if (p.causal) ok = ok && key <= q;
-          if (swa) ok = ok && (q - key) < p.window;
+          const bool ok = visible(q, key, p.N, p.causal, p.window);
           ds = ok ? ds : 0.f;
         }
         dsb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(ds);
@@ -229,6 +230,12 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     }
   }
 }
+
+// Explicit instantiations of every built variant (device code and host launch stubs).
+template __global__ void bwd_dq_kernel<512, 32, true, 4>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<512, 32, false, 4>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<256, 32, true, 4>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<256, 32, false, 4>(const BwdDqParams);
 
 template <int D, int BKV, bool IS_BF16, int NW>
 static hipError_t launch_dq_t(const BwdDqParams& p, hipStream_t stream) {

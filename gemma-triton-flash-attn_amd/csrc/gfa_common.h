@@ -61,20 +61,33 @@ __device__ __forceinline__ float from16(short x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Is key `key` visible to query `q`? (reference attention.py:347-355: key < N; key <= q
+// when causal; q - key < window when causal with a window). Bitwise ops only, so the
+// compiler emits compares and selects instead of per-lane branches.
+__device__ __forceinline__ bool visible(int q, int key, int n, int causal, int window) {
+  const bool in_range = (key < n) & (q < n);
+  const bool before = !causal | (key <= q);
+  const bool in_window = (window <= 0) | (q - key < window);
+  return in_range & before & in_window;
+}
+
 // Keep a kernel-lifetime MFMA operand fragment in AGPRs. MFMA reads A/B operands from
 // AGPRs directly; left alone, the allocator keeps such fragments in the 256 arch VGPRs
 // and spills once the fp32 accumulators fill the AGPR file.
 __device__ __forceinline__ void pin_agpr(i16x8& x) { asm volatile("" : "+a"(x)); }
+__device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x)); }
+__device__ __forceinline__ void pin_vgpr(i16x8& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin_vgpr(f32x16& x) { asm volatile("" : "+v"(x)); }
 
-// XOR swizzle of the 16-byte chunk index inside one LDS tile row. It makes
-//  * ds_read_b128 of one chunk column across 16 consecutive rows hit 16 distinct
-//    4-bank groups, and
-//  * ds_read_b64_tr_b16 of 2 adjacent chunks across 4 consecutive rows
-//    (rows aligned to 4) hit 8 distinct chunk slots.
-// Row bits (0,1) -> chunk bits (1,2); row bit 2 -> chunk bit 3; row bit 3 -> chunk bit 0.
-__device__ __forceinline__ int swz(int row) {
-  return ((row & 3) << 1) | (((row >> 2) & 1) << 3) | ((row >> 3) & 1);
-}
+// XOR swizzle of the 16-byte chunk index inside one LDS tile row (only the low 4 bits
+// of the chunk index change). Two read patterns must be bank-conflict free (64 banks):
+//  * ds_read_b128, 16 lanes per cycle: one chunk column across 16 consecutive rows
+//    -> swz must be a bijection on row bits 0..3;
+//  * ds_read_b64_tr_b16, 32 lanes per cycle: 4 consecutive rows (aligned to 4) x an
+//    aligned group of 4 chunks -> swz bits 2..3 must be a bijection on row bits 0..1.
+// swz swaps the two bit pairs of the row index: chunk bits (2,3) <- row bits (0,1),
+// chunk bits (0,1) <- row bits (2,3).
+__device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
 
 // Byte offset of (row, 16B-chunk c) inside a tile whose rows hold D 16-bit elements.
 template <int D>
@@ -106,34 +119,69 @@ __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(
 // LDS traffic has drained (lgkmcnt): afterwards the whole tile is visible to every wave.
 __device__ __forceinline__ void barrier_tile() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Copy one BKV x D tile (rows row0.., clamped to n_rows-1) from global memory into
-// a swizzled LDS tile. The tile holds BKV * D / 8 chunks of 16 bytes; one wave-level
-// global_load_lds fills 64 consecutive LDS chunks (64 / (D / 8) whole rows), so wave w
-// of NW issues chunk groups w, w + NW, ... The row part of the global address is
-// wave-uniform (scalar); each lane adds only its row-in-group and swizzled chunk.
+// Buffer resource (V#) over one (batch, head) slice of a (B, H, N, D) tensor: raw
+// addressing (stride 0), num_records = bytes up to the end of row n_rows - 1. Buffer loads
+// whose total offset (soffset + voffset) falls past num_records return zeros, so reads of
+// rows >= n_rows need no clamping (their scores are masked anyway).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const uint16_t* base, int64_t row_stride, int n_rows,
+                                                            int row_elems) {
+  const unsigned bytes = (unsigned)(((int64_t)(n_rows - 1) * row_stride + row_elems) * 2);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// Copies BKV x D tiles (rows row0.. of a row-major 16-bit slice) from global memory into
+// swizzled LDS tiles, asynchronously (buffer_load ... lds: no VGPR staging; completion is
+// tracked by vmcnt).
+//
+// A tile holds BKV * D / 8 chunks of 16 bytes. One wave-level instruction fills 64
+// consecutive LDS chunks (RPI = 64 / (D / 8) whole rows); wave w of NW issues chunk groups
+// w, w + NW, ... The row offset of an instruction is a scalar (soffset); each lane adds a
+// per-lane offset (row-in-group, swizzled chunk) computed once per kernel.
 template <int D, int BKV, int NW>
-__device__ __forceinline__ void load_tile_async(const uint16_t* gbase, int64_t row_stride, int row0, int n_rows,
-                                                char GFA_LDS* tile, int wave, int lane) {
-  constexpr int CPR = D / 8;      // chunks per row
-  constexpr int RPI = 64 / CPR;   // rows per wave instruction
-  constexpr int NI = BKV * CPR / (64 * NW);
+struct TileLoader {
+  static constexpr int CPR = D / 8;     // chunks per row
+  static constexpr int RPI = 64 / CPR;  // rows per wave instruction
+  static constexpr int NI = BKV * CPR / (64 * NW);
+  // The swizzle repeats every 16 rows, so the lane offsets repeat every PERIOD instructions.
+  static constexpr int STEP_ROWS = NW * RPI;
+  static constexpr int PERIOD = STEP_ROWS >= 16 ? 1 : 16 / STEP_ROWS;
+  static constexpr int NV = NI < PERIOD ? NI : PERIOD;  // distinct lane offsets
   static_assert(CPR >= 16 && CPR <= 64, "head dim must be 128..512");
   static_assert(BKV * CPR % (64 * NW) == 0, "tile must split evenly over the waves");
-  const int lrow = lane / CPR;
-  const int lc = lane % CPR;
-  const int stride_b = (int)row_stride * 2;
+  static_assert(STEP_ROWS >= 16 ? STEP_ROWS % 16 == 0 : 16 % STEP_ROWS == 0, "swizzle period");
+
+  __amdgpu_buffer_rsrc_t rsrc;
+  unsigned voff[NV];
+  unsigned stride_b;  // bytes between rows
+  int wave;
+
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t row_stride, int n_rows, int wave_, int lane) {
+    wave = wave_;
+    stride_b = (unsigned)(row_stride * 2);
+    rsrc = slice_rsrc(base, row_stride, n_rows, D);
+    const int lrow = lane / CPR;
+    const int lc = lane % CPR;
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int grp = i * NW + wave;
-    // Rows past the end re-read the last row (their scores are masked); the clamp is
-    // branch-free: scalar group base, per-lane row offset min(lrow, last - base).
-    const int srow = min(row0 + grp * RPI, n_rows - 1);
-    const int lr = min(lrow, n_rows - 1 - srow);
-    const char* rbase = reinterpret_cast<const char*>(gbase + (int64_t)srow * row_stride);
-    const unsigned voff = (unsigned)(lr * stride_b + ((lc ^ swz(grp * RPI + lrow)) << 4));
-    dma16(rbase + voff, tile + grp * 1024);
+    for (int i = 0; i < NV; ++i) {
+      const int row = (i * NW + wave) * RPI + lrow;
+      voff[i] = lrow * stride_b + (unsigned)((lc ^ swz(row)) << 4);
+    }
   }
-}
+
+  // Re-point at another slice with the same row stride (dKV streams several heads).
+  __device__ __forceinline__ void rebase(const uint16_t* base, int64_t row_stride, int n_rows) {
+    rsrc = slice_rsrc(base, row_stride, n_rows, D);
+  }
+
+  __device__ __forceinline__ void load(int row0, char GFA_LDS* tile) const {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int grp = i * NW + wave;
+      const unsigned soff = (unsigned)(row0 + grp * RPI) * stride_b;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void GFA_LDS*)(tile + grp * 1024), 16, voff[i % NV], soff, 0, 0);
+    }
+  }
+};
 
 // Partial score block C(32 x 32) = sum_kk A_kk * B_kk over KT k-steps, where A_kk are rows
 // of a swizzled LDS tile (per-lane offsets koff[kk % 8] + 256 * (kk / 8) + extra) and B_kk

@@ -6,50 +6,51 @@
 // and window > 0; the window is ignored when not causal), LSE stored in natural log.
 //
 // MI355X design (not a port of the Triton kernel):
-//  * A workgroup holds NW waves = NW/2 wave PAIRS. A pair owns 32 query rows of one
-//    query head; each wave of the pair owns one half of the head dim. The pairs of a
-//    workgroup are different query heads of the SAME KV head (pack-GQA) and/or
-//    neighbouring query blocks, so each K/V tile is fetched HBM -> LDS once per
-//    workgroup and consumed by every wave.
-//  * Each wave computes a partial S^T = K[:, half] Q[:, half]^T with
-//    v_mfma_f32_32x32x16 (A = K rows from LDS, B = its Q half held in VGPRs for the
-//    whole kernel); the pair swaps partials through LDS so both hold the full scores.
-//    Queries sit on lanes, so softmax statistics are per-lane values and P^T stays in
-//    registers in exactly the B-operand layout of O^T[half] += V^T[half] P^T, whose
-//    A operand is read with the transposing ds_read_b64_tr_b16 from the row-major V tile.
-//    Per wave: 32 x D/2 fp32 accumulator + D/2 Q columns - no spills at D = 512.
-//  * K/V tiles move HBM -> LDS with global_load_lds (no VGPR staging), double
-//    buffered, XOR-swizzled so both LDS read patterns are bank-conflict free.
-//  * Scores are scaled by scale*log2(e) once and exponentiated with v_exp_f32. The
-//    running max is only raised when a tile exceeds it by more than 8 (2^8 headroom), so
-//    the O/l rescale is rare; results are identical up to rounding.
-//  * Causal/window masks are evaluated only on tiles straddling a boundary; fully
-//    hidden tiles are skipped per pair, interior tiles run mask-free.
+//  * A workgroup holds NW waves; each wave owns 32 query rows of one query head over the
+//    whole head dim. The waves of a workgroup are different query heads of the SAME KV
+//    head (pack-GQA) and/or neighbouring query blocks, so each K/V tile is fetched
+//    HBM -> LDS once per workgroup and consumed by NW * 32 query rows.
+//  * The wave computes S^T = K Q^T with v_mfma_f32_32x32x16 (A = K rows from LDS, B = the
+//    wave's Q fragments, resident in VGPRs for the whole kernel). Queries sit on lanes, so
+//    softmax statistics are per-lane values and P^T stays in registers in exactly the
+//    B-operand layout of O^T += V^T P^T, whose A operand is read with the transposing
+//    ds_read_b64_tr_b16 from the row-major V tile. O^T (32 x D fp32) lives in AGPRs.
+//  * K/V tiles move HBM -> LDS with global_load_lds (no VGPR staging), double buffered,
+//    XOR-swizzled so both LDS read patterns are bank-conflict free. The tile loop body is
+//    straight-line code (no per-wave skips, branch-free prefetch) so the accumulators
+//    never leave the AGPRs.
+//  * Softmax uses a fixed per-row reference max instead of a running rescale: the first
+//    tile in which a row sees a key sets m_ref, later tiles use p = exp2(s - m_ref), so the
+//    loop never rescales O. If any row later meets a score above m_ref + kMargin (P could
+//    leave the 16-bit range) the workgroup redoes its rows once with m_ref = the exact row
+//    max observed in the first pass. Exact either way (LSE = m_ref + log2 l); the second
+//    pass is never taken for ordinary inputs.
+//  * Scores are scaled by scale*log2(e) once and exponentiated with v_exp_f32. Causal and
+//    window masks are evaluated only on tiles that straddle a boundary.
 #include "gfa_common.h"
 #include "gfa_params.h"
 #include "gfa_launch.h"
 
 namespace gfa {
 
-template <int D, int BKV, bool IS_BF16, int NW>
-__global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(const FwdParams p) {
-  constexpr int DH = D / 2;      // head-dim columns owned by one wave of a pair
-  constexpr int KTH = DH / 16;   // MFMA k-steps over the half
-  constexpr int DBH = DH / 32;   // 32-row blocks of the O^T half accumulator
-  constexpr int SB = BKV / 32;   // 32-key score blocks per tile
+template <int D, int BKV, bool IS_BF16, int NW, int WPE>
+__global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
+  constexpr int KT = D / 16;   // MFMA k-steps over the head dim
+  constexpr int DB = D / 32;   // 32-row blocks of the O^T accumulator
+  constexpr int SB = BKV / 32; // 32-key score blocks per tile
   constexpr int TILE = BKV * D * 2;
-  constexpr int XCH = SB * 16 * 64 * 4;  // bytes of partial scores one wave publishes
+  // Largest allowed exp2 argument: P stays below 2^15 in fp16 (max 65504); bf16 P and the
+  // fp32 accumulators have range to spare.
+  constexpr float kMargin = IS_BF16 ? 64.0f : 15.0f;
   static_assert(BKV % 32 == 0, "BKV must be a multiple of 32");
-  static_assert(DH % 128 == 0, "head dim must be 256 or 512");
+  static_assert(D % 128 == 0, "head dim must be 128, 256 or 512");
 
-  __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NW * XCH];
+  __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE];
+  __shared__ int redo_flag;
   char GFA_LDS* smem = (char GFA_LDS*)smem_raw;
-  char GFA_LDS* xch = smem + 4 * TILE;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int unit = wave >> 1;  // wave pair
-  const int dh = wave & 1;     // head-dim half
   const int h = lane >> 5;
   const int l32 = lane & 31;
 
@@ -63,8 +64,8 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(const FwdParams p) {
   lid /= p.B;
   const int qsb = p.causal ? (p.g.n_qsb - 1 - lid) : lid;  // causal: longest rows first
 
-  const int head = kvh * p.R + hg * p.g.hpw + (unit % p.g.hpw);
-  const int q0 = (qsb * p.g.qbw + unit / p.g.hpw) * 32;
+  const int head = kvh * p.R + hg * p.g.hpw + (wave % p.g.hpw);
+  const int q0 = (qsb * p.g.qbw + wave / p.g.hpw) * 32;
   const int wg_q_lo = qsb * p.g.qbw * 32;
   const int wg_q_hi = min(p.N, wg_q_lo + p.g.qbw * 32);
 
@@ -77,36 +78,30 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(const FwdParams p) {
   const int t_lo = k_lo / BKV;
   const int t_hi = (k_hi + BKV - 1) / BKV;
 
-  // Keys every query of this pair sees: [all_lo, all_hi).
+  // Keys every query of this wave sees: [all_lo, all_hi).
   const bool active = q0 < p.N;
-  const int q_last = q0 + 31;
   int all_lo = 0, all_hi = p.N;
   if (p.causal) {
     all_hi = min(p.N, q0 + 1);
-    if (swa) all_lo = q_last - p.window + 1;
+    if (swa) all_lo = q0 + 31 - p.window + 1;
   }
+  const int q = q0 + l32;
 
-  // ---- Q half fragments (B operand of S^T = K Q^T), resident for the whole kernel ----
-  i16x8 qf[KTH];
+  // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole kernel ----
+  i16x8 qf[KT];
   {
-    const int qrow = min(q0 + l32, p.N - 1);
-    const uint16_t* qr = p.q + (int64_t)b * p.qv.sb + (int64_t)head * p.qv.sh + (int64_t)qrow * p.qv.sn + dh * DH + 8 * h;
+    const int qrow = min(q, p.N - 1);
+    const uint16_t* qr = p.q + (int64_t)b * p.qv.sb + (int64_t)head * p.qv.sh + (int64_t)qrow * p.qv.sn + 8 * h;
 #pragma unroll
-    for (int kk = 0; kk < KTH; ++kk) qf[kk] = *reinterpret_cast<const i16x8*>(qr + 16 * kk);
+    for (int kk = 0; kk < KT; ++kk) qf[kk] = *reinterpret_cast<const i16x8*>(qr + 16 * kk);
   }
-
-  f32x16 acc[DBH];
-#pragma unroll
-  for (int i = 0; i < DBH; ++i) acc[i] = f32x16{};
-  float m_run = kNegBig;  // running max (log2 domain); identical across the pair and lane halves
-  float l_run = 0.f;      // partial row sum over this lane half's keys
 
   // Per-lane LDS byte offsets inside a tile. The swizzle only touches the low 4 bits of
   // the 16-byte chunk index, so chunk groups of 16 differ by a constant 256 bytes.
-  int koff[8];  // K row l32, chunk dh*DH/8 + 2*kk + h  (+256 * (kk >> 3))
+  int koff[8];  // K row l32, chunk 2*kk + h  (+256 * (kk >> 3))
 #pragma unroll
-  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz(l32)) << 4) + dh * DH * 2;
-  int voffA[4], voffB[4];  // V read transposed: rows 4h + t/4 (+8), columns dh*DH + 32*db + ...
+  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz(l32)) << 4);
+  int voffA[4], voffB[4];  // V read transposed: rows 4h + t/4 (+8), columns 32*db + ...
   {
     const int t16 = lane & 15;
     const int half16 = (lane >> 4) & 1;
@@ -115,129 +110,125 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(const FwdParams p) {
 #pragma unroll
     for (int dl = 0; dl < 4; ++dl) {
       const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
-      voffA[dl] = rA * (2 * D) + ((c ^ swz(rA)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
-      voffB[dl] = rB * (2 * D) + ((c ^ swz(rB)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
+      voffA[dl] = rA * (2 * D) + ((c ^ swz(rA)) << 4) + (t16 & 1) * 8;
+      voffB[dl] = rB * (2 * D) + ((c ^ swz(rB)) << 4) + (t16 & 1) * 8;
     }
   }
-  char GFA_LDS* xmine = xch + wave * XCH + lane * 16;
-  const char GFA_LDS* xpart = xch + (wave ^ 1) * XCH + lane * 16;
 
   const uint16_t* kbase = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh;
   const uint16_t* vbase = p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh;
+  TileLoader<D, BKV, NW> kload, vload;
+  kload.init(kbase, p.kv.sn, p.N, wave, lane);
+  vload.init(vbase, p.vv.sn, p.N, wave, lane);
 
-  if (t_lo < t_hi) {
-    load_tile_async<D, BKV, NW>(kbase, p.kv.sn, t_lo * BKV, p.N, smem, wave, lane);
-    load_tile_async<D, BKV, NW>(vbase, p.vv.sn, t_lo * BKV, p.N, smem + 2 * TILE, wave, lane);
-  }
+  if (threadIdx.x == 0) redo_flag = 0;  // read only after a later barrier
 
-  for (int t = t_lo; t < t_hi; ++t) {
-    const int cur = (t - t_lo) & 1;
-    barrier_tile();  // tile t landed; every wave is done with tile t-1 and its exchange slot
-    {
-      // Prefetch the next tile; the last iteration re-fetches its own tile into the idle
-      // buffer (never read) so the loop body stays branch-free.
-      const int tn = min(t + 1, t_hi - 1);
-      load_tile_async<D, BKV, NW>(kbase, p.kv.sn, tn * BKV, p.N, smem + (cur ^ 1) * TILE, wave, lane);
-      load_tile_async<D, BKV, NW>(vbase, p.vv.sn, tn * BKV, p.N, smem + (2 + (cur ^ 1)) * TILE, wave, lane);
+  f32x16 acc[DB];
+  float m_ref = kNegBig;   // per-row reference max (log2 domain); same in both lane halves
+  float m_seen = kNegBig;  // exact running max (only consulted for the redo pass)
+  float l_run = 0.f;       // partial row sum over this lane half's keys
+  bool ovf = false;
+  // One pass over the workgroup's key tiles. Written once, expanded twice below: the
+  // rare redo pass is a second straight-line copy rather than an outer loop, which keeps
+  // the accumulators' live ranges simple enough to stay in AGPRs.
+  auto run_pass = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
+    l_run = 0.f;
+    if (t_lo < t_hi) {
+      kload.load(t_lo * BKV, smem);
+      vload.load(t_lo * BKV, smem + 2 * TILE);
     }
-    const int k0 = t * BKV;
-    const char GFA_LDS* kt = smem + cur * TILE;
-    const char GFA_LDS* vt = smem + (2 + cur) * TILE;
+    for (int t = t_lo; t < t_hi; ++t) {
+      const int cur = (t - t_lo) & 1;
+      barrier_tile();  // tile t landed; every wave is done reading tile t-1
+      {
+        // Prefetch tile t+1; the last iteration re-fetches its own tile into the idle
+        // buffer (never read) so the body stays branch-free.
+        const int tn = min(t + 1, t_hi - 1);
+        kload.load(tn * BKV, smem + (cur ^ 1) * TILE);
+        vload.load(tn * BKV, smem + (2 + (cur ^ 1)) * TILE);
+      }
+      const int k0 = t * BKV;
+      const char GFA_LDS* kt = smem + cur * TILE;
+      const char GFA_LDS* vt = smem + (2 + cur) * TILE;
 
-    // ---- partial S^T = K[:, half] Q[:, half]^T, published to the partner ----
-    f32x16 s[SB];
-    {
-      // No per-pair skip: a tile this pair cannot see is fully masked below, and the
-      // straight-line body keeps the accumulators resident in registers.
+      // ---- S^T = K Q^T ----
+      f32x16 s[SB];
 #pragma unroll
-      for (int sb = 0; sb < SB; ++sb) {
-        s[sb] = mma_chain_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
+      for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain_lds<IS_BF16, KT, 4>(kt, koff, sb * 32 * (2 * D), qf);
+
+      // ---- softmax against the fixed reference max (lane = query column) ----
+      const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
+      if (need_mask) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x4 v = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
-          *reinterpret_cast<f32x4 GFA_LDS*>(xmine + (sb * 4 + j) * 1024) = v;
+        for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const bool ok = visible(q, key, p.N, p.causal, p.window);
+            s[sb][r] = ok ? s[sb][r] : -INFINITY;
+          }
         }
       }
-    }
-    barrier_lds();  // partials visible
-#pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 v = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + (sb * 4 + j) * 1024);
-        // Same summation order in both waves (a + b == b + a) keeps the pair bit-identical.
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s[sb][4 * j + e] = s[sb][4 * j + e] + v[e];
-      }
-    }
-
-    // ---- online softmax (lane = query column) ----
-    const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
-    if (need_mask) {
-      const int q = q0 + l32;
+      float mt = -INFINITY;
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          bool ok = key < p.N;
-          if (p.causal) ok = ok && key <= q;
-          if (swa) ok = ok && (q - key) < p.window;
-          s[sb][r] = ok ? s[sb][r] : -INFINITY;
+          s[sb][r] *= p.scale_log2;
+          mt = fmaxf(mt, s[sb][r]);
         }
       }
-    }
-    float mt = -INFINITY;
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      // First tile with a visible key fixes m_ref; acc and l are still zero for this row.
+      m_ref = (m_ref == kNegBig && mt > kNegBig) ? mt : m_ref;
+      ovf = ovf || (mt > m_ref + kMargin);
+      m_seen = fmaxf(m_seen, mt);
+      i16x8 pb[BKV / 16];
 #pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
+      for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[sb][r] *= p.scale_log2;
-        mt = fmaxf(mt, s[sb][r]);
+        for (int r = 0; r < 16; ++r) {
+          const float pv = fast_exp2(s[sb][r] - m_ref);
+          l_run += pv;
+          pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
+        }
       }
-    }
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    if (__any(mt > m_run + 8.0f)) {
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = fast_exp2(m_run - m_new);
-      l_run *= alpha;
-#pragma unroll
-      for (int i = 0; i < DBH; ++i) acc[i] *= alpha;
-      m_run = m_new;
-    }
-    i16x8 pb[BKV / 16];
-#pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = fast_exp2(s[sb][r] - m_run);
-        l_run += pv;
-        pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
-      }
-    }
 
-    // ---- O^T[half] += V^T[half] P^T ----
+      // ---- O^T += V^T P^T ----
 #pragma unroll
-    for (int ks = 0; ks < BKV / 16; ++ks) {
+      for (int ks = 0; ks < BKV / 16; ++ks) {
 #pragma unroll
-      for (int db = 0; db < DBH; ++db) {
-        const int imm = ks * 16 * (2 * D) + 256 * (db >> 2);
-        const i16x4 lo = lds_read_tr(vt, voffA[db & 3] + imm);
-        const i16x4 hi = lds_read_tr(vt, voffB[db & 3] + imm);
-        const i16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        acc[db] = mma32<IS_BF16>(a, pb[ks], acc[db]);
+        for (int db = 0; db < DB; ++db) {
+          const int imm = ks * 16 * (2 * D) + 256 * (db >> 2);
+          const i16x4 lo = lds_read_tr(vt, voffA[db & 3] + imm);
+          const i16x4 hi = lds_read_tr(vt, voffB[db & 3] + imm);
+          const i16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          acc[db] = mma32<IS_BF16>(a, pb[ks], acc[db]);
+        }
       }
+      // Keep O^T in AGPRs across iterations (the VGPRs hold Q and the working set).
+#pragma unroll
+      for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
     }
+  };
+  run_pass();
+  // Workgroup vote: does any row need the exact-max redo?
+  if (__any(ovf) && lane == 0) redo_flag = 1;
+  barrier_tile();  // also drains the last (redundant) prefetch before LDS is reused
+  if (redo_flag != 0) {
+    m_ref = m_seen;
+    run_pass();
   }
 
-  // ---- epilogue: normalise, store this wave's O half and (dh == 0) the LSE ----
+  // ---- epilogue: normalise, store O and LSE ----
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const int q = q0 + l32;
   if (active && q < p.N) {
     const float inv = 1.0f / l_tot;
-    uint16_t* orow = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh + (int64_t)q * p.ov.sn + dh * DH;
+    uint16_t* orow = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh + (int64_t)q * p.ov.sn;
 #pragma unroll
-    for (int db = 0; db < DBH; ++db) {
+    for (int db = 0; db < DB; ++db) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         i16x4 o4;
@@ -246,27 +237,38 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(const FwdParams p) {
         *reinterpret_cast<i16x4*>(orow + db * 32 + 8 * g + 4 * h) = o4;
       }
     }
-    if (p.store_lse && h == 0 && dh == 0) {
-      p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + q] = (m_run + __log2f(l_tot)) * kLn2;
+    if (p.store_lse && h == 0) {
+      p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + q] = (m_ref + __log2f(l_tot)) * kLn2;
     }
   }
 }
 
-template <int D, int BKV, bool IS_BF16, int NW>
+// Explicit instantiations of every built variant (both the device code and the host
+// launch stubs must exist for each one).
+#define GFA_FWD_INST(DD, BB, WW, EE)                                              \
+  template __global__ void fwd_kernel<DD, BB, true, WW, EE>(const FwdParams);   \
+  template __global__ void fwd_kernel<DD, BB, false, WW, EE>(const FwdParams);
+GFA_FWD_INST(512, 32, 4, 1)
+GFA_FWD_INST(256, 64, 4, 1)
+GFA_FWD_INST(256, 32, 4, 1)
+#undef GFA_FWD_INST
+
+template <int D, int BKV, bool IS_BF16, int NW, int WPE>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
+  hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
   return hipGetLastError();
 }
 
+// Built forward variants: (head dim, keys per tile, waves per workgroup, waves per SIMD).
 hipError_t launch_fwd(const FwdParams& p, int D, int bkv, int nw, bool bf16, hipStream_t stream) {
-#define GFA_FWD_CASE(DD, BB, WW)                                                                       \
-  if (D == DD && bkv == BB && nw == WW) {                                                              \
-    return bf16 ? launch_fwd_t<DD, BB, true, WW>(p, stream) : launch_fwd_t<DD, BB, false, WW>(p, stream); \
+#define GFA_FWD_CASE(DD, BB, WW, EE)                                                      \
+  if (D == DD && bkv == BB && nw == WW) {                                                 \
+    return bf16 ? launch_fwd_t<DD, BB, true, WW, EE>(p, stream)                           \
+                : launch_fwd_t<DD, BB, false, WW, EE>(p, stream);                         \
   }
-  GFA_FWD_CASE(512, 32, 4)
-  GFA_FWD_CASE(512, 32, 8)
-  GFA_FWD_CASE(256, 32, 4)
-  GFA_FWD_CASE(256, 64, 4)
+  GFA_FWD_CASE(512, 32, 4, 1)
+  GFA_FWD_CASE(256, 64, 4, 1)
+  GFA_FWD_CASE(256, 32, 4, 1)
 #undef GFA_FWD_CASE
   return hipErrorInvalidValue;
 }

@@ -52,14 +52,14 @@ def _pow2_divisor_le(r: int, cap: int) -> int:
     return x
 
 
-def query_grid(batch: int, heads_q: int, heads_kv: int, seq_len: int, waves: int) -> dict:
+def query_grid(batch: int, heads_q: int, heads_kv: int, seq_len: int, units: int) -> dict:
     """Workgroup decomposition of the forward / dQ kernels (pack-GQA).
 
-    A workgroup holds waves/2 wave pairs; each pair owns 32 query rows of one query head.
-    The pairs are ``hpw`` heads of one KV head times ``qbw`` neighbouring 32-row blocks.
+    A workgroup holds ``units`` 32-row query blocks (one per wave in the forward kernel,
+    one per wave pair in the dQ kernel): ``hpw`` query heads of one KV head times ``qbw``
+    neighbouring 32-row blocks.
     """
     r = heads_q // heads_kv
-    units = waves // 2
     hpw = _pow2_divisor_le(r, units)
     qbw = units // hpw
     n_qsb = -(-seq_len // (32 * qbw))
@@ -85,7 +85,7 @@ def get_config(batch: int, heads_q: int, heads_kv: int, seq_len: int, head_dim: 
     """Everything the library decides for one problem (same keys as ``gfa_config``)."""
     c = lookup(head_dim)
     fq = query_grid(batch, heads_q, heads_kv, seq_len, c.fwd_waves)
-    dq = query_grid(batch, heads_q, heads_kv, seq_len, c.dq_waves)
+    dq = query_grid(batch, heads_q, heads_kv, seq_len, c.dq_waves // 2)
     return {
         "head_dim": head_dim,
         "fwd_block_q": fq["block_q"],

@@ -1,0 +1,162 @@
+"""CPU checks of the C ABI boundary and the host-side API (no kernel is launched).
+
+* libgfa.so loads and exports every entry point declared in include/gfa.h;
+* the ctypes structs match the C layout (sizeof / offsetof from a gcc-compiled probe);
+* gfa_config agrees with the Python registry;
+* invalid arguments are rejected before any launch, with the documented status codes;
+* the Python API raises on inputs the engine cannot take (no silent fallback).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+import torch
+
+import gemma_triton_flash_attn_amd as gfa
+from gemma_triton_flash_attn_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gfa.h")
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    text = open(HEADER).read()
+    declared = sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(gfa_\w+)\s*\(", text, re.M)))
+    assert declared, "no declarations parsed"
+    assert set(declared) == set(_lib.EXPORTED)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.gfa_version() == int(re.search(r"#define GFA_VERSION (\d+)", text).group(1))
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_struct_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(f'''
+#include <stdio.h>
+#include <stddef.h>
+#include "{HEADER}"
+int main(void) {{
+  printf("%zu %zu %zu\\n", sizeof(gfa_fwd_args), sizeof(gfa_bwd_args), sizeof(gfa_config_info));
+  printf("%zu %zu %zu %zu\\n", offsetof(gfa_fwd_args, lse_ld), offsetof(gfa_fwd_args, stream),
+         offsetof(gfa_bwd_args, stages), offsetof(gfa_bwd_args, workspace_bytes));
+  return 0;
+}}
+''')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    sizes = [int(x) for x in out]
+    assert sizes[:3] == [ctypes.sizeof(_lib.FwdArgs), ctypes.sizeof(_lib.BwdArgs), ctypes.sizeof(_lib.ConfigInfo)]
+    assert sizes[3:] == [_lib.FwdArgs.lse_ld.offset, _lib.FwdArgs.stream.offset, _lib.BwdArgs.stages.offset,
+                         _lib.BwdArgs.workspace_bytes.offset]
+
+
+@pytest.mark.parametrize("shape", [(1, 32, 4, 16384, 512), (1, 16, 8, 16384, 256), (2, 6, 3, 33, 256),
+                                   (1, 4, 4, 1, 512), (1, 8, 1, 1024, 512), (3, 16, 2, 32768, 512)])
+def test_config_matches_python_registry(shape):
+    assert _lib.config(*shape) == gfa.get_config(*shape)
+
+
+def _fwd_args(**over):
+    a = _lib.FwdArgs()
+    a.q = a.k = a.v = a.o = 256  # fake, 16-byte aligned: validation happens before any launch
+    a.lse = 512
+    a.batch, a.heads_q, a.heads_kv, a.seq_len, a.head_dim = 1, 8, 2, 64, 512
+    for s in ("q_strides", "k_strides", "v_strides", "o_strides"):
+        setattr(a, s, _lib.Strides(8 * 64 * 512, 64 * 512, 512))
+    a.causal, a.window, a.scale, a.dtype, a.lse_ld = 1, 0, 512 ** -0.5, _lib.GFA_DTYPE_BF16, 64
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(head_dim=128), 2),
+    (dict(heads_q=6, heads_kv=4), 1),
+    (dict(seq_len=0), 1),
+    (dict(dtype=7), 1),
+    (dict(window=-1), 1),
+    (dict(q=260), 1),                     # misaligned pointer
+    (dict(lse_ld=16), 1),                 # lse rows shorter than GFA_LSE_LD(N)
+    (dict(scale=float("nan")), 1),
+    (dict(block_kv=48), 2),               # no such forward tile
+    (dict(k_strides=_lib.Strides(8, 8, 4)), 1),  # row stride not a multiple of 8 elements
+])
+def test_fwd_rejects_bad_arguments(over, status):
+    lib = _lib.load()
+    a = _fwd_args(**over)
+    assert lib.gfa_fwd(ctypes.byref(a)) == status
+    assert lib.gfa_last_error()
+    assert lib.gfa_fwd(None) == 1
+
+
+def test_bwd_rejects_bad_arguments():
+    lib = _lib.load()
+    a = _lib.BwdArgs()
+    for name in ("q", "k", "v", "o", "dout", "dq", "dk", "dv"):
+        setattr(a, name, 256)
+    for s in ("q_strides", "k_strides", "v_strides", "o_strides", "do_strides", "dq_strides", "dk_strides",
+              "dv_strides"):
+        setattr(a, s, _lib.Strides(8 * 64 * 512, 64 * 512, 512))
+    a.batch, a.heads_q, a.heads_kv, a.seq_len, a.head_dim = 1, 8, 1, 64, 512
+    a.causal, a.scale, a.dtype = 1, 512 ** -0.5, _lib.GFA_DTYPE_BF16
+    a.lse_ld = 64
+    # lse / delta missing
+    assert lib.gfa_bwd(ctypes.byref(a)) == 1
+    a.lse, a.delta = 512, 1024
+    a.stages = 4
+    assert lib.gfa_bwd(ctypes.byref(a)) == 1
+    a.stages = 0
+    a.q_splits = 3
+    assert lib.gfa_bwd(ctypes.byref(a)) == 1
+    a.q_splits = 4  # needs a workspace
+    assert lib.gfa_bwd(ctypes.byref(a)) == 3
+    need = lib.gfa_bwd_workspace_size(1, 8, 1, 64, 512, 1, 0, 4)
+    assert need == 4 * 2 * 1 * 1 * 64 * 512 * 4
+    a.workspace, a.workspace_bytes = 4096, need - 1
+    assert lib.gfa_bwd(ctypes.byref(a)) == 3
+
+
+def test_python_api_validation_needs_no_gpu():
+    q = torch.randn(1, 4, 16, 256, dtype=torch.bfloat16)
+    k = torch.randn(1, 2, 16, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        gfa.flash_attn_gqa_train(q, k, k, causal=True)
+    with pytest.raises(TypeError):
+        gfa.attention_flash_gqa(q, k.float(), k, causal=True)
+    with pytest.raises(ValueError, match="head_dim"):
+        gfa.attention_flash_gqa(q[..., :128], k[..., :128], k[..., :128])
+    with pytest.raises(ValueError, match="multiple"):
+        gfa.attention_flash_gqa(q[:, :3], k, k)
+    with pytest.raises(ValueError):
+        gfa.attention(q, k, k)  # MHA form only
+
+
+def test_hf_adapter_rejects_unsupported_features():
+    from types import SimpleNamespace
+
+    mod = SimpleNamespace(head_dim=256, is_causal=True)
+    q = torch.zeros(1, 2, 4, 256)
+    with pytest.raises(NotImplementedError):
+        gfa.triton_gqa_attention(mod, q, q, q, None, softcap=30.0)
+    with pytest.raises(NotImplementedError):
+        gfa.triton_gqa_attention(mod, q, q, q, None, dropout=0.1)
+
+
+def test_register_into_transformers():
+    pytest.importorskip("transformers")
+    from transformers import AttentionInterface
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    gfa.register_triton_attention()
+    assert ALL_ATTENTION_FUNCTIONS.get_interface("triton_gqa", None) is gfa.triton_gqa_attention
+    assert "triton_gqa" in AttentionInterface._global_mapping
+    gfa.register_triton_attention("gfa_custom")
+    assert ALL_ATTENTION_FUNCTIONS.get_interface("gfa_custom", None) is gfa.triton_gqa_attention
