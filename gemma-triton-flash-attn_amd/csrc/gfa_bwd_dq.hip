@@ -7,13 +7,13 @@
 //   dS_ij   = P_ij * (dO_i.v_j - delta_i)                 (masked -> 0, cast to input dtype)
 //   dQ_i    = s * sum_j dS_ij k_j
 //
-// MI355X design: the same wave-pair decomposition as the forward kernel. A pair owns 32
-// query rows of one head; each wave keeps its head-dim half of Q and dO in VGPRs (B
-// operands of S^T = K Q^T and dP^T = V dO^T, lane = query), computes partial S^T and dP^T
+// MI355X design: a wave pair owns 32 query rows of one head; each wave keeps its
+// head-dim half of Q and dO in VGPRs (B operands of S^T = K Q^T and dP^T = V dO^T,
+// lane = query), computes partial S^T and dP^T
 // over its half, and swaps them with the partner through LDS. P^T and dS^T then live on
 // the query lanes with per-lane LSE and delta, and dQ^T[half] += K^T[half] dS^T reads its
 // A operand with ds_read_b64_tr_b16 from the same row-major K tile that fed S^T. K and V
-// tiles are double-buffered in LDS via global_load_lds.
+// tiles are double-buffered in LDS via buffer loads that write LDS directly.
 #include "gfa_common.h"
 #include "gfa_params.h"
 #include "gfa_launch.h"

@@ -103,12 +103,6 @@ __device__ __forceinline__ i16x4 lds_read_tr(const char GFA_LDS* base, int off) 
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 GFA_LDS*)(base + off));
 }
 
-// Asynchronous 16-byte global -> LDS copy. The LDS destination of lane L is
-// lds_wave_base + 16 * L (lds_wave_base must be wave-uniform).
-__device__ __forceinline__ void dma16(const void* gsrc, char GFA_LDS* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(gsrc, (void GFA_LDS*)lds_wave_base, 16, 0, 0);
-}
-
 // Workgroup barrier for LDS producer/consumer hand-offs. It waits only for this
 // wave's outstanding LDS operations (lgkmcnt), unlike __syncthreads(), whose release
 // fence also drains every outstanding global load (including in-flight tile prefetches).
@@ -206,6 +200,59 @@ __device__ __forceinline__ f32x16 mma_chain_lds(const char GFA_LDS* tile, const 
     }
   }
   return c0 + c1;
+}
+
+// Single-accumulator variant of mma_chain_lds (back-to-back dependent MFMAs; 16 fewer
+// live registers).
+template <bool IS_BF16, int KT, int PF>
+__device__ __forceinline__ f32x16 mma_chain1_lds(const char GFA_LDS* tile, const int (&koff)[8], int extra,
+                                                 const i16x8 (&bf)[KT]) {
+  static_assert(PF <= KT, "bad chain shape");
+  f32x16 c = f32x16{};
+  i16x8 a[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, koff[i & 7] + 256 * (i >> 3) + extra);
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const i16x8 cur = a[kk % PF];
+    if (kk + PF < KT) a[kk % PF] = lds_read16(tile, koff[(kk + PF) & 7] + 256 * ((kk + PF) >> 3) + extra);
+    c = mma32<IS_BF16>(cur, bf[kk], c);
+  }
+  return c;
+}
+
+// A operand of O^T += V^T P^T (or any product whose A operand is a row-major LDS tile read
+// transposed): two ds_read_b64_tr_b16 at the per-lane offsets offA / offB (+ imm).
+__device__ __forceinline__ i16x8 tr_frag(const char GFA_LDS* tile, int offA, int offB, int imm) {
+  const i16x4 lo = lds_read_tr(tile, offA + imm);
+  const i16x4 hi = lds_read_tr(tile, offB + imm);
+  return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// acc[db] += A(ks, db) * B[ks] over ks < NKS, db < DB, where A(ks, db) is read transposed
+// from `tile` (row block ks * 16, column block db * 32 of a D-wide row-major tile). The
+// reads run PF products ahead of the MFMAs.
+template <bool IS_BF16, int D, int DB, int NKS, int PF>
+__device__ __forceinline__ void mma_tr_accumulate(f32x16 (&acc)[DB], const char GFA_LDS* tile, const int (&offA)[4],
+                                                  const int (&offB)[4], const i16x8 (&bop)[NKS]) {
+  constexpr int N = NKS * DB;
+  static_assert(PF <= N, "prefetch deeper than the product count");
+  i16x8 a[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    const int ks = i / DB, db = i % DB;
+    a[i] = tr_frag(tile, offA[db & 3], offB[db & 3], ks * 16 * (2 * D) + 256 * (db >> 2));
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int ks = i / DB, db = i % DB;
+    const i16x8 cur = a[i % PF];
+    if (i + PF < N) {
+      const int ks2 = (i + PF) / DB, db2 = (i + PF) % DB;
+      a[i % PF] = tr_frag(tile, offA[db2 & 3], offB[db2 & 3], ks2 * 16 * (2 * D) + 256 * (db2 >> 2));
+    }
+    acc[db] = mma32<IS_BF16>(cur, bop[ks], acc[db]);
+  }
 }
 
 // Map the hardware workgroup id to a logical id so that GROUP consecutive logical

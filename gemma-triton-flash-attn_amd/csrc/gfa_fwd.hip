@@ -15,8 +15,9 @@
 //    softmax statistics are per-lane values and P^T stays in registers in exactly the
 //    B-operand layout of O^T += V^T P^T, whose A operand is read with the transposing
 //    ds_read_b64_tr_b16 from the row-major V tile. O^T (32 x D fp32) lives in AGPRs.
-//  * K/V tiles move HBM -> LDS with global_load_lds (no VGPR staging), double buffered,
-//    XOR-swizzled so both LDS read patterns are bank-conflict free. The tile loop body is
+//  * K/V tiles move HBM -> LDS with buffer loads that write LDS directly (no VGPR
+//    staging; the buffer range check turns rows past the sequence end into zeros), double
+//    buffered, XOR-swizzled so both LDS read patterns are bank-conflict free. The tile loop body is
 //    straight-line code (no per-wave skips, branch-free prefetch) so the accumulators
 //    never leave the AGPRs.
 //  * Softmax uses a fixed per-row reference max instead of a running rescale: the first
@@ -45,9 +46,19 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   static_assert(BKV % 32 == 0, "BKV must be a multiple of 32");
   static_assert(D % 128 == 0, "head dim must be 128, 256 or 512");
 
-  __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE];
+  // Four distinct LDS objects (not one array indexed by a buffer id): with the loop
+  // unrolled by two every access names its buffer statically, so the compiler's wait
+  // insertion can tell the in-flight prefetch (into the other buffer) from the tile being
+  // read and does not stall on it.
+  __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
+  __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
+  __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
+  __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
   __shared__ int redo_flag;
-  char GFA_LDS* smem = (char GFA_LDS*)smem_raw;
+  char GFA_LDS* const K0 = (char GFA_LDS*)k_lds0;
+  char GFA_LDS* const K1 = (char GFA_LDS*)k_lds1;
+  char GFA_LDS* const V0 = (char GFA_LDS*)v_lds0;
+  char GFA_LDS* const V1 = (char GFA_LDS*)v_lds1;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -76,7 +87,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     if (swa) k_lo = max(0, wg_q_lo - p.window + 1);
   }
   const int t_lo = k_lo / BKV;
-  const int t_hi = (k_hi + BKV - 1) / BKV;
+  // Even tile count (the loop is unrolled by two): an odd range gets one extra tile past
+  // the workgroup's keys, which is fully masked (and zero-filled past the sequence end).
+  const int t_hi = t_lo + ((((k_hi + BKV - 1) / BKV) - t_lo + 1) & ~1);
 
   // Keys every query of this wave sees: [all_lo, all_hi).
   const bool active = q0 < p.N;
@@ -131,86 +144,83 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   // One pass over the workgroup's key tiles. Written once, expanded twice below: the
   // rare redo pass is a second straight-line copy rather than an outer loop, which keeps
   // the accumulators' live ranges simple enough to stay in AGPRs.
+  // One key tile: wait for it, prefetch the next one into the other buffers, then
+  // S^T = K Q^T, softmax against the fixed reference max, O^T += V^T P^T.
+  auto step = [&](int t, const char GFA_LDS* kt, const char GFA_LDS* vt, char GFA_LDS* kn,
+                  char GFA_LDS* vn) __attribute__((always_inline)) {
+    barrier_tile();  // tile t landed; every wave is done reading the other buffers
+    {
+      // The last step re-fetches its own tile into the idle buffers (never read) so the
+      // body stays branch-free.
+      const int tn = min(t + 1, t_hi - 1);
+      kload.load(tn * BKV, kn);
+      vload.load(tn * BKV, vn);
+    }
+    const int k0 = t * BKV;
+    f32x16 s[SB];
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4>(kt, koff, sb * 32 * (2 * D), qf);
+
+    const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
+    if (need_mask) {
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const bool ok = visible(q, key, p.N, p.causal, p.window);
+          s[sb][r] = ok ? s[sb][r] : -INFINITY;
+        }
+      }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[sb][r] *= p.scale_log2;
+        mt = fmaxf(mt, s[sb][r]);
+      }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    // First tile with a visible key fixes m_ref; acc and l are still zero for this row.
+    m_ref = (m_ref == kNegBig && mt > kNegBig) ? mt : m_ref;
+    ovf = ovf || (mt > m_ref + kMargin);
+    m_seen = fmaxf(m_seen, mt);
+    i16x8 pb[BKV / 16];
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = fast_exp2(s[sb][r] - m_ref);
+        l_run += pv;
+        pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
+      }
+    }
+    mma_tr_accumulate<IS_BF16, D, DB, BKV / 16, 2>(acc, vt, voffA, voffB, pb);
+    // Keep O^T in AGPRs across iterations (the VGPRs hold Q and the working set).
+#pragma unroll
+    for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
+  };
+
+  // One pass over the workgroup's key tiles. Written once, expanded twice below: the
+  // rare redo pass is a second straight-line copy rather than an outer loop, which keeps
+  // the accumulators' live ranges simple enough to stay in AGPRs.
   auto run_pass = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
     l_run = 0.f;
     if (t_lo < t_hi) {
-      kload.load(t_lo * BKV, smem);
-      vload.load(t_lo * BKV, smem + 2 * TILE);
+      kload.load(t_lo * BKV, K0);
+      vload.load(t_lo * BKV, V0);
     }
-    for (int t = t_lo; t < t_hi; ++t) {
-      const int cur = (t - t_lo) & 1;
-      barrier_tile();  // tile t landed; every wave is done reading tile t-1
-      {
-        // Prefetch tile t+1; the last iteration re-fetches its own tile into the idle
-        // buffer (never read) so the body stays branch-free.
-        const int tn = min(t + 1, t_hi - 1);
-        kload.load(tn * BKV, smem + (cur ^ 1) * TILE);
-        vload.load(tn * BKV, smem + (2 + (cur ^ 1)) * TILE);
-      }
-      const int k0 = t * BKV;
-      const char GFA_LDS* kt = smem + cur * TILE;
-      const char GFA_LDS* vt = smem + (2 + cur) * TILE;
-
-      // ---- S^T = K Q^T ----
-      f32x16 s[SB];
-#pragma unroll
-      for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain_lds<IS_BF16, KT, 4>(kt, koff, sb * 32 * (2 * D), qf);
-
-      // ---- softmax against the fixed reference max (lane = query column) ----
-      const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
-      if (need_mask) {
-#pragma unroll
-        for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            const bool ok = visible(q, key, p.N, p.causal, p.window);
-            s[sb][r] = ok ? s[sb][r] : -INFINITY;
-          }
-        }
-      }
-      float mt = -INFINITY;
-#pragma unroll
-      for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s[sb][r] *= p.scale_log2;
-          mt = fmaxf(mt, s[sb][r]);
-        }
-      }
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      // First tile with a visible key fixes m_ref; acc and l are still zero for this row.
-      m_ref = (m_ref == kNegBig && mt > kNegBig) ? mt : m_ref;
-      ovf = ovf || (mt > m_ref + kMargin);
-      m_seen = fmaxf(m_seen, mt);
-      i16x8 pb[BKV / 16];
-#pragma unroll
-      for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = fast_exp2(s[sb][r] - m_ref);
-          l_run += pv;
-          pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
-        }
-      }
-
-      // ---- O^T += V^T P^T ----
-#pragma unroll
-      for (int ks = 0; ks < BKV / 16; ++ks) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const int imm = ks * 16 * (2 * D) + 256 * (db >> 2);
-          const i16x4 lo = lds_read_tr(vt, voffA[db & 3] + imm);
-          const i16x4 hi = lds_read_tr(vt, voffB[db & 3] + imm);
-          const i16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          acc[db] = mma32<IS_BF16>(a, pb[ks], acc[db]);
-        }
-      }
-      // Keep O^T in AGPRs across iterations (the VGPRs hold Q and the working set).
-#pragma unroll
-      for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
+    for (int t = t_lo; t < t_hi; t += 2) {
+      // Scheduling fences keep the two tile steps from being interleaved, which would
+      // raise register pressure past the VGPR budget.
+      step(t, K0, V0, K1, V1);
+      __builtin_amdgcn_sched_barrier(0);
+      step(t + 1, K1, V1, K0, V0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   run_pass();
