@@ -199,7 +199,7 @@ def attention_flash_gqa(q, k, v, causal=False, slide_size=0, BLOCK_Q=None, BLOCK
     ``BLOCK_KV`` selects one of the built LDS tile widths for this head dim. ``BLOCK_Q``,
     ``BLOCK_D``, ``num_warps`` and ``num_stages`` are Triton launch knobs of the reference;
     they are accepted for call compatibility and have no effect here (the gfx950 kernels
-    always run 32-row wave pairs with the registry's tiles).
+    always run 32-row waves or wave pairs with the registry's tiles).
     """
     _check_inputs(q, k, v)
     D = q.shape[3]

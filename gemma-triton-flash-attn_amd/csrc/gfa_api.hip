@@ -31,8 +31,9 @@ int ok() {
 // ---------------------------------------------------------------------------------
 // HEAD_DIM-keyed registry (mirrors registry.py). Replaces the reference's if/else tile
 // tables (/root/reference/flash_attn/attention.py:561-579, 1445-1451, 1498-1504,
-// 1536-1564) with MI355X tiles: every kernel works on wave pairs that split the head
-// dim, 32 rows per pair, NW waves per workgroup.
+// 1536-1564) with MI355X tiles. Forward: one wave per 32 query rows over the full head
+// dim; dQ: wave pairs splitting the head dim, 32 query rows per pair; dK/dV: wave pairs
+// splitting the work by role (P/dV and dS/dK), 32 keys per pair. NW waves per workgroup.
 // ---------------------------------------------------------------------------------
 struct Entry {
   int head_dim;

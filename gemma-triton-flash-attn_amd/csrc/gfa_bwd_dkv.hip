@@ -13,15 +13,17 @@
 // dkv_reduce_kernel sums them in a fixed order (deterministic, no atomics; the reference
 // uses atomic_add into 16-bit dK/dV, attention.py:1206-1209).
 //
-// MI355X design: wave pairs again. A pair owns 32 keys; each wave keeps its head-dim half
-// of K and V in VGPRs (B operands of S = Q K^T and dP = dO V^T, lane = key) and its half of
-// the dK^T / dV^T accumulators. Per LDS tile of BQ queries the wave computes partial S and
-// dP, swaps them with its partner, forms P and dS on the key lanes (LSE / delta are
-// per-register row values read from global memory), then
-//   dV^T[half] += dO^T[half] P   and   dK^T[half] += Q^T[half] dS,
-// reading the A operands with ds_read_b64_tr_b16 from the row-major dO and Q tiles that
-// fed the score products. All R query heads of the KV head stream through the same
-// workgroup (pack-GQA), so K/V are read once and dK/dV need no cross-head reduction.
+// MI355X design: a wave pair owns 32 keys and splits the work by role, not by head dim.
+// Both waves keep a full-head-dim stationary B operand in VGPRs (lane = key): role 0 the
+// K rows, role 1 the V rows. Per LDS tile of BQ queries
+//   role 0: S = Q K^T (A = Q tile rows), P = exp2(S*scale*log2e - LSE*log2e) masked,
+//           P handed to the partner through LDS (fp32), then dV^T += dO^T P;
+//   role 1: dP = dO V^T (A = dO tile rows), dS = P (dP - delta), then dK^T += Q^T dS;
+// the dV^T / dK^T accumulators (32 keys x D, fp32) fill the AGPRs, and the A operands of
+// the two accumulations are read with ds_read_b64_tr_b16 from the same row-major tiles
+// that fed the score products. The only cross-wave traffic is the one-way P hand-off, and
+// no softmax work is duplicated. All R query heads of the KV head stream through the
+// same workgroup (pack-GQA), so K/V are read once and dK/dV need no cross-head reduction.
 #include "gfa_common.h"
 #include "gfa_params.h"
 #include "gfa_launch.h"
@@ -30,27 +32,25 @@ namespace gfa {
 
 template <int D, int BQ, bool IS_BF16, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams p) {
-  constexpr int DH = D / 2;
-  constexpr int KTH = DH / 16;
-  constexpr int DBH = DH / 32;
+  constexpr int KT = D / 16;   // MFMA k-steps of the score products (full head dim)
+  constexpr int DB = D / 32;   // 32-row blocks of the dV^T / dK^T accumulator
   constexpr int SB = BQ / 32;  // 32-query score blocks per tile
   constexpr int TILE = BQ * D * 2;
-  constexpr int XHALF = SB * 16 * 64 * 4;
-  constexpr int XCH = 2 * XHALF;
+  constexpr int PX = SB * 64 * 64;  // fp32 P hand-off of one pair: SB * 16 floats per lane
   constexpr int NU = NW / 2;
   static_assert(BQ % 32 == 0, "BQ must be a multiple of 32");
-  static_assert(DH % 128 == 0, "head dim must be 256 or 512");
+  static_assert(D % 128 == 0, "head dim must be 256 or 512");
 
-  __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NW * XCH];
+  __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NU * PX];
   char GFA_LDS* smem = (char GFA_LDS*)smem_raw;
-  char GFA_LDS* xch = smem + 4 * TILE;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int unit = wave >> 1;
-  const int dh = wave & 1;
+  const int role = wave & 1;  // 0: S, P and dV;  1: dP, dS and dK
   const int h = lane >> 5;
   const int l32 = lane & 31;
+  char GFA_LDS* px = smem + 4 * TILE + unit * PX + lane * 16;
 
   // ---- workgroup -> (split, b, kv head, key block); early key blocks (most work) first ----
   int lid = xcd_remap(blockIdx.x, p.nblocks, 4);
@@ -90,34 +90,25 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
   }
   const bool pair_full = k_last < p.N;
 
-  // ---- K and V halves (B operands: lane = key), resident ----
-  i16x8 kf[KTH], vf[KTH];
+  // ---- stationary B operand (lane = key, full head dim): K rows for role 0, V rows for role 1 ----
+  i16x8 kvf[KT];
   {
-    const uint16_t* kr = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh + (int64_t)krow * p.kv.sn + dh * DH + 8 * h;
-    const uint16_t* vr = p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh + (int64_t)krow * p.vv.sn + dh * DH + 8 * h;
+    const uint16_t* base = role == 0 ? p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh + (int64_t)krow * p.kv.sn
+                                     : p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh + (int64_t)krow * p.vv.sn;
+    const uint16_t* r = base + 8 * h;
 #pragma unroll
-    for (int kk = 0; kk < KTH; ++kk) {
-      kf[kk] = *reinterpret_cast<const i16x8*>(kr + 16 * kk);
-      vf[kk] = *reinterpret_cast<const i16x8*>(vr + 16 * kk);
-    }
-#pragma unroll
-    for (int kk = 0; kk < KTH; ++kk) {
-      pin_agpr(kf[kk]);
-      pin_agpr(vf[kk]);
-    }
+    for (int kk = 0; kk < KT; ++kk) kvf[kk] = *reinterpret_cast<const i16x8*>(r + 16 * kk);
   }
 
-  f32x16 dk[DBH], dv[DBH];
+  // dV^T (role 0) or dK^T (role 1), 32 keys x D, in AGPRs.
+  f32x16 acc[DB];
 #pragma unroll
-  for (int i = 0; i < DBH; ++i) {
-    dk[i] = f32x16{};
-    dv[i] = f32x16{};
-  }
+  for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
 
-  int roff[8];  // Q / dO tile rows (A operand of S, dP): row l32, chunk dh*DH/8 + 2*kk + h
+  int roff[8];  // tile rows (A operand of S / dP): row l32, chunk 2*kk + h  (+256 * (kk >> 3))
 #pragma unroll
-  for (int kl = 0; kl < 8; ++kl) roff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz(l32)) << 4) + dh * DH * 2;
-  int toffA[4], toffB[4];  // Q / dO tiles read transposed (A operands of dK^T, dV^T)
+  for (int kl = 0; kl < 8; ++kl) roff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz(l32)) << 4);
+  int toffA[4], toffB[4];  // tiles read transposed (A operands of dV^T, dK^T)
   {
     const int t16 = lane & 15;
     const int half16 = (lane >> 4) & 1;
@@ -126,12 +117,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
 #pragma unroll
     for (int dl = 0; dl < 4; ++dl) {
       const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
-      toffA[dl] = rA * (2 * D) + ((c ^ swz(rA)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
-      toffB[dl] = rB * (2 * D) + ((c ^ swz(rB)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
+      toffA[dl] = rA * (2 * D) + ((c ^ swz(rA)) << 4) + (t16 & 1) * 8;
+      toffB[dl] = rB * (2 * D) + ((c ^ swz(rB)) << 4) + (t16 & 1) * 8;
     }
   }
-  char GFA_LDS* xmine = xch + wave * XCH + lane * 16;
-  const char GFA_LDS* xpart = xch + (wave ^ 1) * XCH + lane * 16;
 
   TileLoader<D, BQ, NW> qload, dload;
   qload.init(p.q, p.qv.sn, p.N, wave, lane);
@@ -142,6 +131,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
     q_start = qt * BQ;
     return base + (int64_t)b * v.sb + (int64_t)(kvh * p.R + r) * v.sh;
   };
+  // Row statistic this wave needs: LSE for role 0 (P), delta for role 1 (dS).
+  const float* stat_base = role == 0 ? p.lse : p.delta;
 
   if (it_lo < it_hi) {
     int qs0;
@@ -155,7 +146,19 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
 
   for (int it = it_lo; it < it_hi; ++it) {
     const int cur = (it - it_lo) & 1;
-    barrier_tile();
+    barrier_tile();  // tile `it` landed; every wave is done with the other buffers and px
+    const int head = kvh * p.R + it / nqt;
+    const int q0 = (qt_lo + it % nqt) * BQ;
+    // Row statistics of this tile (rows q0 + sb*32 + 8g + 4h + 0..3; rows padded to a
+    // multiple of 32), issued before the prefetch so they are not queued behind it.
+    f32x4 st[SB][4];
+    {
+      const float* srow = stat_base + ((int64_t)b * p.Hq + head) * p.lse_ld + q0 + 4 * h;
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) st[sb][g] = *reinterpret_cast<const f32x4*>(srow + sb * 32 + 8 * g);
+    }
     {
       // Prefetch the next tile; the last iteration re-fetches its own tile into the idle
       // buffer (never read) so the loop body stays branch-free.
@@ -168,136 +171,101 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
       qload.load(qs1, smem + (cur ^ 1) * TILE);
       dload.load(qs1, smem + (2 + (cur ^ 1)) * TILE);
     }
-    const int head = kvh * p.R + it / nqt;
-    const int q0 = (qt_lo + it % nqt) * BQ;
     const char GFA_LDS* qt = smem + cur * TILE;
     const char GFA_LDS* dt = smem + (2 + cur) * TILE;
+    // role 0: S = Q K^T from the Q tile, then dV^T += dO^T P reads the dO tile transposed.
+    // role 1: dP = dO V^T from the dO tile, then dK^T += Q^T dS reads the Q tile transposed.
+    const char GFA_LDS* ct = role == 0 ? qt : dt;
+    const char GFA_LDS* tt = role == 0 ? dt : qt;
 
-    // Every tile runs the same straight-line code (no per-pair skip): a tile a pair cannot
-    // see is fully masked below. Branch-free bodies keep the dK/dV accumulators resident.
-    f32x16 s[SB], dp[SB];
+    f32x16 s[SB];
 #pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
-      s[sb] = mma_chain_lds<IS_BF16, KTH, 4>(qt, roff, sb * 32 * (2 * D), kf);
-      dp[sb] = mma_chain_lds<IS_BF16, KTH, 4>(dt, roff, sb * 32 * (2 * D), vf);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 vs = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
-        const f32x4 vd = {dp[sb][4 * j], dp[sb][4 * j + 1], dp[sb][4 * j + 2], dp[sb][4 * j + 3]};
-        *reinterpret_cast<f32x4 GFA_LDS*>(xmine + (sb * 4 + j) * 1024) = vs;
-        *reinterpret_cast<f32x4 GFA_LDS*>(xmine + XHALF + (sb * 4 + j) * 1024) = vd;
-      }
-    }
-    barrier_lds();
-#pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 vs = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + (sb * 4 + j) * 1024);
-        const f32x4 vd = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + XHALF + (sb * 4 + j) * 1024);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s[sb][4 * j + e] = s[sb][4 * j + e] + vs[e];
-          dp[sb][4 * j + e] = dp[sb][4 * j + e] + vd[e];
-        }
-      }
-    }
+    for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4>(ct, roff, sb * 32 * (2 * D), kvf);
 
-    // ---- P and dS on the key lanes; rows (queries) are per-register ----
-    // LSE / delta rows are padded to a multiple of 32, so whole 4-row groups are readable.
-    const float* lse_row = p.lse + ((int64_t)b * p.Hq + head) * p.lse_ld;
-    const float* del_row = p.delta + ((int64_t)b * p.Hq + head) * p.lse_ld;
-#pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int qq = q0 + sb * 32 + 8 * g + 4 * h;  // rows qq .. qq+3 of this lane
-        const f32x4 lse4 = *reinterpret_cast<const f32x4*>(lse_row + qq);
-        const f32x4 del4 = *reinterpret_cast<const f32x4*>(del_row + qq);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * g + e;
-          const float pv = fast_exp2(s[sb][r] * p.scale_log2 - lse4[e] * kLog2e);
-          s[sb][r] = pv;
-          dp[sb][r] = pv * (dp[sb][r] - del4[e]);
-        }
-      }
-    }
-    const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
-    if (need_mask) {
+    if (role == 0) {
+      // P on the key lanes (rows = queries per register), masked, handed to the partner in fp32.
+      const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qi = q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          const bool ok = visible(qi, key, p.N, p.causal, p.window);
-          s[sb][r] = ok ? s[sb][r] : 0.f;
-          dp[sb][r] = ok ? dp[sb][r] : 0.f;
+        for (int r = 0; r < 16; ++r) s[sb][r] = fast_exp2(s[sb][r] * p.scale_log2 - st[sb][r >> 2][r & 3] * kLog2e);
+      }
+      if (need_mask) {
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int qi = q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            s[sb][r] = visible(qi, key, p.N, p.causal, p.window) ? s[sb][r] : 0.f;
+          }
+        }
+      }
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 v = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
+          *reinterpret_cast<f32x4 GFA_LDS*>(px + (sb * 4 + j) * 1024) = v;
         }
       }
     }
-    i16x8 pb[BQ / 16], dsb[BQ / 16];
+    barrier_lds();  // P of this tile is in px
+    if (role == 1) {
+      // dS = P * (dP - delta); P == 0 (masked, or underflowed) gives exactly 0, also for
+      // padding rows whose delta is not defined.
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 pv = *reinterpret_cast<const f32x4 GFA_LDS*>(px + (sb * 4 + j) * 1024);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * j + e;
+            s[sb][r] = pv[e] != 0.f ? pv[e] * (s[sb][r] - st[sb][j][e]) : 0.f;
+          }
+        }
+      }
+    }
+    i16x8 pb[BQ / 16];
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(s[sb][r]);
-        dsb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(dp[sb][r]);
-      }
+      for (int r = 0; r < 16; ++r) pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(s[sb][r]);
     }
-
-    // ---- dV^T[half] += dO^T[half] P ; dK^T[half] += Q^T[half] dS ----
+    mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 2>(acc, tt, toffA, toffB, pb);
 #pragma unroll
-    for (int ks = 0; ks < BQ / 16; ++ks) {
-#pragma unroll
-      for (int db = 0; db < DBH; ++db) {
-        const int imm = ks * 16 * (2 * D) + 256 * (db >> 2);
-        const i16x4 dlo = lds_read_tr(dt, toffA[db & 3] + imm);
-        const i16x4 dhi = lds_read_tr(dt, toffB[db & 3] + imm);
-        const i16x8 ad = {dlo[0], dlo[1], dlo[2], dlo[3], dhi[0], dhi[1], dhi[2], dhi[3]};
-        dv[db] = mma32<IS_BF16>(ad, pb[ks], dv[db]);
-        const i16x4 qlo = lds_read_tr(qt, toffA[db & 3] + imm);
-        const i16x4 qhi = lds_read_tr(qt, toffB[db & 3] + imm);
-        const i16x8 aq = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
-        dk[db] = mma32<IS_BF16>(aq, dsb[ks], dk[db]);
-      }
-    }
+    for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
   }
 
   // ---- epilogue: lane = key, registers = head-dim rows 32*db + 8*g + 4*h + e ----
   if (active && key < p.N) {
+    const float osc = role == 0 ? 1.f : p.scale;  // dK carries the softmax scale
     if (p.q_splits == 1) {
-      uint16_t* dkrow = p.dk + (int64_t)b * p.dkv.sb + (int64_t)kvh * p.dkv.sh + (int64_t)key * p.dkv.sn + dh * DH;
-      uint16_t* dvrow = p.dv + (int64_t)b * p.dvv.sb + (int64_t)kvh * p.dvv.sh + (int64_t)key * p.dvv.sn + dh * DH;
+      uint16_t* orow = role == 0
+                           ? p.dv + (int64_t)b * p.dvv.sb + (int64_t)kvh * p.dvv.sh + (int64_t)key * p.dvv.sn
+                           : p.dk + (int64_t)b * p.dkv.sb + (int64_t)kvh * p.dkv.sh + (int64_t)key * p.dkv.sn;
 #pragma unroll
-      for (int db = 0; db < DBH; ++db) {
+      for (int db = 0; db < DB; ++db) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          i16x4 k4, v4;
+          i16x4 o4;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            k4[e] = to16<IS_BF16>(dk[db][4 * g + e] * p.scale);
-            v4[e] = to16<IS_BF16>(dv[db][4 * g + e]);
-          }
-          *reinterpret_cast<i16x4*>(dkrow + db * 32 + 8 * g + 4 * h) = k4;
-          *reinterpret_cast<i16x4*>(dvrow + db * 32 + 8 * g + 4 * h) = v4;
+          for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[db][4 * g + e] * osc);
+          *reinterpret_cast<i16x4*>(orow + db * 32 + 8 * g + 4 * h) = o4;
         }
       }
     } else {
       // fp32 partials [split][dk|dv][b][kvh][key][d], dK already scaled.
       const int64_t plane = (int64_t)p.B * p.Hkv * p.N * D;
-      const int64_t rowoff = (((int64_t)b * p.Hkv + kvh) * p.N + key) * D + dh * DH;
-      float* pk = p.part + (int64_t)split * 2 * plane + rowoff;
-      float* pv = pk + plane;
+      const int64_t rowoff = (((int64_t)b * p.Hkv + kvh) * p.N + key) * D;
+      float* dst = p.part + (int64_t)split * 2 * plane + (role == 0 ? plane : 0) + rowoff;
 #pragma unroll
-      for (int db = 0; db < DBH; ++db) {
+      for (int db = 0; db < DB; ++db) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const f32x4 k4 = {dk[db][4 * g] * p.scale, dk[db][4 * g + 1] * p.scale, dk[db][4 * g + 2] * p.scale,
-                            dk[db][4 * g + 3] * p.scale};
-          const f32x4 v4 = {dv[db][4 * g], dv[db][4 * g + 1], dv[db][4 * g + 2], dv[db][4 * g + 3]};
-          *reinterpret_cast<f32x4*>(pk + db * 32 + 8 * g + 4 * h) = k4;
-          *reinterpret_cast<f32x4*>(pv + db * 32 + 8 * g + 4 * h) = v4;
+          const f32x4 v4 = {acc[db][4 * g] * osc, acc[db][4 * g + 1] * osc, acc[db][4 * g + 2] * osc,
+                            acc[db][4 * g + 3] * osc};
+          *reinterpret_cast<f32x4*>(dst + db * 32 + 8 * g + 4 * h) = v4;
         }
       }
     }

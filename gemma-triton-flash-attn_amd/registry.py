@@ -3,8 +3,10 @@
 The reference keeps its tile choices as if/else tables keyed on HEAD_DIM inside the
 launch code (/root/reference/flash_attn/attention.py:561-579 inference forward,
 1445-1451 training forward, 1498-1504 dQ, 1536-1564 dKV, 1576-1587 Q_SPLITS). Here the
-same role is one explicit table. Each entry names the tiles of the three gfx950 kernels;
-every kernel works on wave pairs that split the head dim, 32 rows per pair.
+same role is one explicit table. Each entry names the tiles of the three gfx950 kernels:
+the forward runs one wave per 32 query rows over the full head dim, the dQ kernel wave
+pairs that split the head dim (32 query rows per pair), the dK/dV kernel wave pairs that
+split the work by role (32 keys per pair).
 
 The C library holds the same table (csrc/gfa_api.hip, kRegistry); ``gfa_config`` reports
 what the library will use and the tests assert the two agree.
