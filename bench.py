@@ -21,8 +21,14 @@ from __future__ import annotations
 import argparse
 import json
 import math
+import csv
+import glob
 import os
+import shutil
+import signal
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -55,6 +61,16 @@ def kernel_flops(w):
     (query, key) pair; forward 2 products, dQ 3 (S, dP, dQ), dKV 4 (S, dP, dV, dK)."""
     unit = charged_flops(w, "fwd") / 2.0  # = 2*D*pairs (causal convention)
     return {"fwd": 2 * unit, "dq": 3 * unit, "dkv": 4 * unit}
+
+
+def kernel_bytes(w):
+    """Algorithmic HBM bytes per launch of each kernel: every tensor the kernel must touch,
+    read or written once (16-bit Q/K/V/O/dO/dQ/dK/dV, fp32 LSE and delta)."""
+    B, Hq, Hkv, N, D = w["B"], w["Hq"], w["Hkv"], w["N"], w["D"]
+    qsz, kvsz, rows = 2 * B * Hq * N * D, 2 * B * Hkv * N * D, 4 * B * Hq * N
+    return {"fwd": 2 * qsz + 2 * kvsz + rows,             # Q, K, V in; O, LSE out
+            "dq": 4 * qsz + 2 * kvsz + 2 * rows,          # Q, O, dO, K, V, LSE in; dQ, delta out
+            "dkv": 2 * qsz + 4 * kvsz + 2 * rows}         # Q, dO, K, V, LSE, delta in; dK, dV out
 
 
 def make_inputs(w, device):
@@ -137,6 +153,117 @@ def bench_workload(name, w, steps, warmup, device, kernels=True):
     return res
 
 
+KERNEL_TAGS = {"fwd": "fwd_kernel", "dq": "bwd_dq_kernel", "dkv": "bwd_dkv_kernel"}
+PMC_COUNTERS = ("FETCH_SIZE", "WRITE_SIZE")  # KiB per dispatch, one counter per rocprofv3 pass
+
+
+def pmc_child(name, calib_mib):
+    """Body run under ``rocprofv3 --pmc``: one launch of each kernel at ``name``'s shape,
+    then one plain elementwise copy (torch.neg, fp32) of ``calib_mib`` MiB whose counter
+    reading calibrates the counter (known bytes: calib_mib MiB read + calib_mib MiB written)."""
+    import torch
+
+    from gemma_triton_flash_attn_amd import _lib
+    from gemma_triton_flash_attn_amd.attention import _backward, _forward
+
+    w = WORKLOADS[name]
+    dev = torch.device("cuda:0")
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[w["dtype"]]
+    gen = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(w["B"], w["Hq"], w["N"], w["D"], device=dev, dtype=dt, generator=gen)
+    k = torch.randn(w["B"], w["Hkv"], w["N"], w["D"], device=dev, dtype=dt, generator=gen)
+    v = torch.randn(w["B"], w["Hkv"], w["N"], w["D"], device=dev, dtype=dt, generator=gen)
+    do = torch.randn(w["B"], w["Hq"], w["N"], w["D"], device=dev, dtype=dt, generator=gen)
+    scale = w["D"] ** -0.5
+    o, lse = _forward(q, k, v, w["causal"], w["window"], scale, store_lse=True)
+    bufs = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+            torch.empty(lse.shape, dtype=torch.float32, device=dev))
+    _backward(q, k, v, o, lse, do, w["causal"], w["window"], scale, stages=_lib.GFA_BWD_DQ, out=bufs)
+    _backward(q, k, v, o, lse, do, w["causal"], w["window"], scale, stages=_lib.GFA_BWD_DKV, out=bufs)
+    torch.cuda.synchronize()
+    del q, k, v, do, o, lse, bufs
+    src = torch.empty((calib_mib << 20) // 4, dtype=torch.float32, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(f"[pmc-child] {name}: fwd, dq, dkv and a {calib_mib} MiB copy done", file=sys.stderr, flush=True)
+    return 0
+
+
+def _read_pmc_csv(outdir, counter):
+    """{kernel name: [per-dispatch value]} and the name of the last dispatch, from the
+    rocprofv3 counter-collection CSV under ``outdir``."""
+    files = glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise RuntimeError(f"no counter_collection.csv under {outdir}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            rows += [r for r in csv.DictReader(fh) if r.get("Counter_Name") == counter]
+    if not rows:
+        raise RuntimeError(f"counter {counter} missing in {files}")
+    rows.sort(key=lambda r: int(r.get("Dispatch_Id", 0)))
+    vals = {}
+    for r in rows:
+        vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return vals, rows[-1]["Kernel_Name"]
+
+
+def measure_traffic(name, calib_mib=1024, timeout_s=180, keep_dir=None):
+    """HBM traffic per launch of each kernel, from two rocprofv3 --pmc passes (FETCH_SIZE,
+    then WRITE_SIZE) over ``pmc_child``, each scaled by what the same counter reads for a
+    copy of known size. Runs before this process touches the GPU; returns None (with a
+    message) when rocprofv3 is missing or a pass fails."""
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        print("[bench] traffic: rocprofv3 not found", file=sys.stderr, flush=True)
+        return None
+    copy_known_kib = calib_mib * 1024.0  # the copy reads this much and writes this much
+    out = {"calib_mib": calib_mib, "kernels": {}}
+    env = dict(os.environ, TMPDIR="/tmp")
+    for counter in PMC_COUNTERS:
+        d = keep_dir and os.path.join(keep_dir, counter.lower())
+        d = d or tempfile.mkdtemp(prefix="gfa_pmc_", dir="/tmp")
+        cmd = [exe, "--pmc", counter, "-d", d, "-o", "pmc", "--output-format", "csv", "--",
+               sys.executable, os.path.abspath(__file__), "--pmc-child", name, "--copy-calib-mib", str(calib_mib)]
+        print(f"[bench] traffic pass {counter}: {' '.join(cmd[:-6])} -- python bench.py --pmc-child {name}",
+              file=sys.stderr, flush=True)
+        proc = subprocess.Popen(cmd, cwd="/tmp", env=env, start_new_session=True,
+                                stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, text=True)
+        try:
+            _, err = proc.communicate(timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.wait()
+            print(f"[bench] traffic: {counter} pass timed out", file=sys.stderr, flush=True)
+            return None
+        try:
+            vals, last = _read_pmc_csv(d, counter)
+        except RuntimeError as e:
+            print(f"[bench] traffic: {counter} pass rc={proc.returncode}: {e}\n{(err or '')[-1500:]}",
+                  file=sys.stderr, flush=True)
+            return None
+        finally:
+            if not keep_dir:
+                shutil.rmtree(d, ignore_errors=True)
+        copy_kib = vals[last][-1]
+        factor = copy_known_kib / copy_kib if copy_kib > 0 else float("nan")
+        out[f"{counter.lower()}_factor"] = factor
+        out["copy_kernel"] = last
+        for kname, tag in KERNEL_TAGS.items():
+            hits = [v for kn, v in vals.items() if tag in kn and "reduce" not in kn]
+            if not hits:
+                continue
+            kib = sum(hits[0]) / len(hits[0])
+            ent = out["kernels"].setdefault(kname, {})
+            ent[f"{counter.lower()}_kib_raw"] = kib
+            ent[f"{counter.lower()}_bytes"] = kib * 1024.0 * factor
+    for ent in out["kernels"].values():
+        if "fetch_size_bytes" in ent and "write_size_bytes" in ent:
+            ent["traffic_bytes"] = ent["fetch_size_bytes"] + ent["write_size_bytes"]
+    return out
+
+
 def cpu_baseline(budget_s=12.0):
     """Reference CPU path (SDPA math, fp32) on config 1: B1 N1024 Hq32 Hkv4 D512 causal."""
     from oracle.cpu_baseline import time_forward
@@ -162,13 +289,24 @@ def main(argv=None):
     ap.add_argument("--no-kernels", action="store_true", help="skip per-kernel timing")
     ap.add_argument("--workloads", default="d512_causal_gqa8_n16k,d256_swa1024_gqa2_n16k",
                     help="comma list of workloads to time (the first one must be the headline)")
-    ap.add_argument("--copy-calib-mib", type=int, default=0,
-                    help="also run a plain device copy of this many MiB (rocprof FETCH/WRITE_SIZE calibration)")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc passes that measure HBM traffic per kernel")
+    ap.add_argument("--copy-calib-mib", type=int, default=1024,
+                    help="size of the plain copy that calibrates FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--pmc-dir", default=None, help="keep the rocprofv3 counter CSVs in this directory")
+    ap.add_argument("--pmc-child", default=None, metavar="WORKLOAD",
+                    help="internal: the program profiled by the traffic passes")
     args = ap.parse_args(argv)
+    if args.pmc_child:
+        return pmc_child(args.pmc_child, args.copy_calib_mib)
     if args.gpus != 1:
         print(f"bench.py: this engine is a single-GPU build; --gpus {args.gpus} is not supported "
               "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
         return 2
+
+    head = "d512_causal_gqa8_n16k"
+    # The counter passes are child processes started before this process touches the GPU.
+    traffic = None if args.no_traffic else measure_traffic(head, args.copy_calib_mib, keep_dir=args.pmc_dir)
 
     import torch
 
@@ -176,7 +314,6 @@ def main(argv=None):
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     device = torch.device("cuda:0")
-    head = "d512_causal_gqa8_n16k"
     names = [n for n in args.workloads.split(",") if n]
     for n in names:
         if n not in WORKLOADS:
@@ -186,15 +323,6 @@ def main(argv=None):
     for n in names:
         steps = args.steps if n != "d256_swa1024_gqa2_n16k" else max(args.steps, 10)
         results[n] = bench_workload(n, WORKLOADS[n], steps, args.warmup, device, kernels=not args.no_kernels)
-    if args.copy_calib_mib:
-        nbytes = args.copy_calib_mib << 20
-        src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=device).normal_()
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(f"[bench] copy calibration: 3 x {args.copy_calib_mib} MiB device copies", file=sys.stderr, flush=True)
-        del src, dst
     if head not in results:
         print(json.dumps({"metric": METRIC, "workloads": results}), flush=True)
         return 0
@@ -207,10 +335,24 @@ def main(argv=None):
     if "kernels" in h:
         dom = max(h["kernels"], key=lambda kname: h["kernels"][kname]["ms"])
         kd = h["kernels"][dom]
+        kb = kernel_bytes(WORKLOADS[head])
+        tk = (traffic or {}).get("kernels", {})
+        for kname, ent in h["kernels"].items():
+            ent["algorithmic_bytes"] = kb[kname]
+            if "traffic_bytes" in tk.get(kname, {}):
+                ent["traffic_bytes"] = round(tk[kname]["traffic_bytes"])
+                ent["traffic_over_algorithmic"] = round(tk[kname]["traffic_bytes"] / kb[kname], 3)
         roofline = {"bound": "mfma", "kernel": dom, "achieved": round(kd["tflops"], 2), "peak": PEAK_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(kd["tflops"] / PEAK_TFLOPS, 4), "traffic": None,
+                    "unit": "TFLOP/s", "frac": round(kd["tflops"] / PEAK_TFLOPS, 4),
+                    "traffic": kd.get("traffic_bytes"),
+                    "algorithmic_bytes": kb[dom],
                     "ms_per_launch": round(kd["ms"], 4),
                     "flops_per_launch": kernel_flops(WORKLOADS[head])[dom]}
+        if traffic:
+            roofline["traffic_calibration"] = {k_: round(traffic[k_], 4) for k_ in ("fetch_size_factor",
+                                                                                     "write_size_factor")
+                                               if k_ in traffic}
+            roofline["traffic_calibration"]["copy_mib"] = traffic["calib_mib"]
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
