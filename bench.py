@@ -264,6 +264,65 @@ def measure_traffic(name, calib_mib=1024, timeout_s=180, keep_dir=None):
     return out
 
 
+# Config 5: a random-init model of the Gemma-4-E2B architecture (35 decoder layers: 28
+# sliding-window layers with head dim 256, window 512, and 7 full-causal layers with head
+# dim 512, the pattern four sliding then one full; GQA 8:1; per-layer input embeddings).
+# Built locally from transformers' Gemma4TextConfig with random weights (no checkpoint).
+E2E_CONFIG = dict(vocab_size=262144, hidden_size=1536, intermediate_size=6144, num_hidden_layers=35,
+                  num_attention_heads=8, num_key_value_heads=1, head_dim=256, global_head_dim=512,
+                  sliding_window=512, hidden_size_per_layer_input=256, vocab_size_per_layer_input=262144,
+                  layer_types=["full_attention" if (i + 1) % 5 == 0 else "sliding_attention" for i in range(35)],
+                  max_position_embeddings=32768)
+
+
+def bench_e2e(device, seq_len=16384, steps=3, warmup=1):
+    """Config 5: forward latency and peak HBM of the E2B-architecture model at N=seq_len,
+    every attention layer swapped to this engine by the one-call HF registration."""
+    import torch
+    from transformers import Gemma4ForCausalLM, Gemma4TextConfig
+
+    import gemma_triton_flash_attn_amd as gfa
+
+    print(f"[bench] e2e: Gemma-4-E2B architecture, random init, N={seq_len}", file=sys.stderr, flush=True)
+    gfa.register_triton_attention()
+    cfg = Gemma4TextConfig(**E2E_CONFIG)
+    torch.manual_seed(0)
+    with torch.device(device):
+        model = Gemma4ForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval()
+    for m in model.modules():
+        c = getattr(m, "config", None)
+        if c is not None and hasattr(c, "_attn_implementation"):
+            c._attn_implementation = "triton_gqa"
+    n_params = sum(p.numel() for p in model.parameters())
+    ids = torch.randint(0, cfg.vocab_size, (1, seq_len), generator=torch.Generator().manual_seed(0)).to(device)
+
+    def fwd():
+        with torch.no_grad():
+            return model(input_ids=ids, logits_to_keep=1, use_cache=False).logits
+
+    out = fwd()
+    ok = bool(torch.isfinite(out).all())
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(device)
+    base = torch.cuda.memory_allocated(device)
+    ms = time_loop(fwd, steps, warmup)
+    peak = torch.cuda.max_memory_allocated(device)
+    res = {"workload": "gemma4_e2b_arch_random_init_fwd", "seq_len": seq_len, "batch": 1, "dtype": "bf16",
+           "ms": round(ms, 2), "tokens_per_s": round(seq_len / ms * 1e3, 1),
+           "peak_hbm_gib": round(peak / 2 ** 30, 3), "weights_gib": round(base / 2 ** 30, 3),
+           "params": n_params, "finite": ok, "layers": cfg.num_hidden_layers,
+           "attention": "triton_gqa (this engine via register_triton_attention)",
+           "logits": "last position only (logits_to_keep=1)", "config": {k: v for k, v in E2E_CONFIG.items()
+                                                                          if k != "layer_types"},
+           "layer_pattern": "4 x sliding_attention (D=256, W=512) then 1 x full_attention (D=512), x7"}
+    print(f"[bench] e2e: {res['ms']} ms, {res['tokens_per_s']} tok/s, peak {res['peak_hbm_gib']} GiB "
+          f"(weights {res['weights_gib']} GiB)", file=sys.stderr, flush=True)
+    del model, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(budget_s=12.0):
     """Reference CPU path (SDPA math, fp32) on config 1: B1 N1024 Hq32 Hkv4 D512 causal."""
     from oracle.cpu_baseline import time_forward
@@ -293,6 +352,7 @@ def main(argv=None):
                     help="skip the two rocprofv3 --pmc passes that measure HBM traffic per kernel")
     ap.add_argument("--copy-calib-mib", type=int, default=1024,
                     help="size of the plain copy that calibrates FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 model forward (Gemma-4-E2B arch)")
     ap.add_argument("--pmc-dir", default=None, help="keep the rocprofv3 counter CSVs in this directory")
     ap.add_argument("--pmc-child", default=None, metavar="WORKLOAD",
                     help="internal: the program profiled by the traffic passes")
@@ -330,6 +390,13 @@ def main(argv=None):
         for name in ("c2_d512_causal_gqa8_n8k", "c4_d512_causal_gqa8_n32k"):
             results[name] = bench_workload(name, WORKLOADS[name], args.steps, args.warmup, device, kernels=False)
 
+    e2e = None
+    if not args.no_e2e:
+        try:
+            e2e = bench_e2e(device)
+        except Exception as exc:  # reported, never fatal for the headline line
+            print(f"[bench] e2e failed: {type(exc).__name__}: {exc}", file=sys.stderr, flush=True)
+            e2e = {"error": f"{type(exc).__name__}: {exc}"}
     h = results[head]
     roofline = None
     if "kernels" in h:
@@ -381,6 +448,7 @@ def main(argv=None):
                       for k_, r in results.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "e2e": e2e,
     }
     print(json.dumps(line), flush=True)
     return 0
