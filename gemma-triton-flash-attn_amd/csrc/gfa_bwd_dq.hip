@@ -94,8 +94,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   }
 #pragma unroll
   for (int kk = 0; kk < KTH; ++kk) {
-    pin_agpr(qf[kk]);
-    pin_agpr(df[kk]);
+    pin_vgpr(qf[kk]);
+    pin_vgpr(df[kk]);
   }
   dpart += __shfl_xor(dpart, 32);
   // Pair exchange of the two head-dim halves of delta (through the exchange area).
@@ -160,8 +160,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       // straight-line body keeps the accumulators resident in registers.
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
-        s[sb] = mma_chain_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
-        dp[sb] = mma_chain_lds<IS_BF16, KTH, 4>(vt, koff, sb * 32 * (2 * D), df);
+        s[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
+        dp[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(vt, koff, sb * 32 * (2 * D), df);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const f32x4 vs = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
@@ -187,20 +187,26 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     }
 
     const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[sb][r] = fast_exp2(s[sb][r] * p.scale_log2 - lse_log2) * (dp[sb][r] - delta);
+    }
+    if (need_mask) {
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          s[sb][r] = visible(q, key, p.N, p.causal, p.window) ? s[sb][r] : 0.f;
+        }
+      }
+    }
     i16x8 dsb[BKV / 16];
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = fast_exp2(s[sb][r] * p.scale_log2 - lse_log2);
-        float ds = pv * (dp[sb][r] - delta);
-        if (need_mask) {
-          const int key = k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          const bool ok = visible(q, key, p.N, p.causal, p.window);
-          ds = ok ? ds : 0.f;
-        }
-        dsb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(ds);
-      }
+      for (int r = 0; r < 16; ++r) dsb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(s[sb][r]);
     }
 
 #pragma unroll
