@@ -125,62 +125,37 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
   TileLoader<D, BQ, NW> qload, dload;
   qload.init(p.q, p.qv.sn, p.N, wave, lane);
   dload.init(p.dout, p.dov.sn, p.N, wave, lane);
-  auto tile_src = [&](int it, const uint16_t* base, const RowView& v, int& q_start) {
-    const int r = it / nqt;
-    const int qt = qt_lo + it % nqt;
-    q_start = qt * BQ;
-    return base + (int64_t)b * v.sb + (int64_t)(kvh * p.R + r) * v.sh;
-  };
+  const uint16_t* q_kv = p.q + (int64_t)b * p.qv.sb + (int64_t)kvh * p.R * p.qv.sh;
+  const uint16_t* d_kv = p.dout + (int64_t)b * p.dov.sb + (int64_t)kvh * p.R * p.dov.sh;
   // Row statistic this wave needs: LSE for role 0 (P), delta for role 1 (dS).
-  const float* stat_base = role == 0 ? p.lse : p.delta;
+  const float* stat_kv = (role == 0 ? p.lse : p.delta) + ((int64_t)b * p.Hq + (int64_t)kvh * p.R) * p.lse_ld;
 
+  // Iteration `it` covers head kvh*R + r of query tile qt, it = r * nqt + (qt - qt_lo);
+  // (r_c, qt_c) walk it incrementally.
+  int r_c = nqt > 0 ? it_lo / nqt : 0;
+  int qt_c = nqt > 0 ? qt_lo + it_lo % nqt : 0;
   if (it_lo < it_hi) {
-    int qs0;
-    const uint16_t* qb = tile_src(it_lo, p.q, p.qv, qs0);
-    const uint16_t* db = tile_src(it_lo, p.dout, p.dov, qs0);
-    qload.rebase(qb, p.qv.sn, p.N);
-    dload.rebase(db, p.dov.sn, p.N);
-    qload.load(qs0, smem);
-    dload.load(qs0, smem + 2 * TILE);
+    qload.rebase(q_kv + (int64_t)r_c * p.qv.sh, p.qv.sn, p.N);
+    dload.rebase(d_kv + (int64_t)r_c * p.dov.sh, p.dov.sn, p.N);
+    qload.load(qt_c * BQ, smem);
+    dload.load(qt_c * BQ, smem + 2 * TILE);
   }
 
-  for (int it = it_lo; it < it_hi; ++it) {
-    const int cur = (it - it_lo) & 1;
-    barrier_tile();  // tile `it` landed; every wave is done with the other buffers and px
-    const int head = kvh * p.R + it / nqt;
-    const int q0 = (qt_lo + it % nqt) * BQ;
-    // Row statistics of this tile (rows q0 + sb*32 + 8g + 4h + 0..3; rows padded to a
-    // multiple of 32), issued before the prefetch so they are not queued behind it.
-    f32x4 st[SB][4];
-    {
-      const float* srow = stat_base + ((int64_t)b * p.Hq + head) * p.lse_ld + q0 + 4 * h;
-#pragma unroll
-      for (int sb = 0; sb < SB; ++sb)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) st[sb][g] = *reinterpret_cast<const f32x4*>(srow + sb * 32 + 8 * g);
-    }
-    {
-      // Prefetch the next tile; the last iteration re-fetches its own tile into the idle
-      // buffer (never read) so the loop body stays branch-free.
-      const int itn = min(it + 1, it_hi - 1);
-      int qs1;
-      const uint16_t* qb = tile_src(itn, p.q, p.qv, qs1);
-      const uint16_t* db = tile_src(itn, p.dout, p.dov, qs1);
-      qload.rebase(qb, p.qv.sn, p.N);
-      dload.rebase(db, p.dov.sn, p.N);
-      qload.load(qs1, smem + (cur ^ 1) * TILE);
-      dload.load(qs1, smem + (2 + (cur ^ 1)) * TILE);
-    }
-    const char GFA_LDS* qt = smem + cur * TILE;
-    const char GFA_LDS* dt = smem + (2 + cur) * TILE;
-    // role 0: S = Q K^T from the Q tile, then dV^T += dO^T P reads the dO tile transposed.
-    // role 1: dP = dO V^T from the dO tile, then dK^T += Q^T dS reads the Q tile transposed.
-    const char GFA_LDS* ct = role == 0 ? qt : dt;
-    const char GFA_LDS* tt = role == 0 ? dt : qt;
+  // One query tile: prefetch the next tile into (qn, dn), score chain from ct, P / dS,
+  // accumulation reading tt transposed. The views are restrict-qualified: the compiler
+  // then knows that no read of ct / tt / pxr touches the prefetch targets and does not
+  // wait for the prefetch before reading the current tile.
+  auto tile_step = [&](const char GFA_LDS* __restrict__ ct, const char GFA_LDS* __restrict__ tt,
+                       char GFA_LDS* __restrict__ qn, char GFA_LDS* __restrict__ dn, char GFA_LDS* __restrict__ pxr,
+                       int row_n, int q0, const f32x4 (&st)[SB][4]) __attribute__((always_inline)) {
+    qload.load(row_n, qn);
+    dload.load(row_n, dn);
 
     f32x16 s[SB];
+    __builtin_amdgcn_sched_barrier(0);  // the two MFMA pipelines are scheduled on their own
 #pragma unroll
-    for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4>(ct, roff, sb * 32 * (2 * D), kvf);
+    for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(ct, roff, sb * 32 * (2 * D), kvf);
+    __builtin_amdgcn_sched_barrier(0);
 
     if (role == 0) {
       // P on the key lanes (rows = queries per register), masked, handed to the partner in fp32.
@@ -205,7 +180,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const f32x4 v = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
-          *reinterpret_cast<f32x4 GFA_LDS*>(px + (sb * 4 + j) * 1024) = v;
+          *reinterpret_cast<f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024) = v;
         }
       }
     }
@@ -217,7 +192,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
       for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const f32x4 pv = *reinterpret_cast<const f32x4 GFA_LDS*>(px + (sb * 4 + j) * 1024);
+          const f32x4 pv = *reinterpret_cast<const f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * j + e;
@@ -232,10 +207,48 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
 #pragma unroll
       for (int r = 0; r < 16; ++r) pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(s[sb][r]);
     }
-    mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 2>(acc, tt, toffA, toffB, pb);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 4, 1>(acc, tt, toffA, toffB, pb);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
+  };
+
+  for (int it = it_lo; it < it_hi; ++it) {
+    const int cur = (it - it_lo) & 1;
+    barrier_tile();  // tile `it` landed; every wave is done with the other buffers and px
+    const int q0 = qt_c * BQ;
+    // Row statistics of this tile (rows q0 + sb*32 + 8g + 4h + 0..3; rows padded to a
+    // multiple of 32), issued before the prefetch so they are not queued behind it.
+    f32x4 st[SB][4];
+    {
+      const float* srow = stat_kv + (int64_t)r_c * p.lse_ld + q0 + 4 * h;
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) st[sb][g] = *reinterpret_cast<const f32x4*>(srow + sb * 32 + 8 * g);
+    }
+    // Next tile; the last iteration re-fetches its own tile into the idle buffer (never
+    // read) so the loop body stays branch-free.
+    int r_n = r_c, qt_n = qt_c + 1;
+    if (qt_n == qt_hi) {
+      qt_n = qt_lo;
+      ++r_n;
+    }
+    if (it + 1 >= it_hi) {
+      r_n = r_c;
+      qt_n = qt_c;
+    }
+    qload.rebase(q_kv + (int64_t)r_n * p.qv.sh, p.qv.sn, p.N);
+    dload.rebase(d_kv + (int64_t)r_n * p.dov.sh, p.dov.sn, p.N);
+    r_c = r_n;
+    qt_c = qt_n;
+    // role 0: S = Q K^T from the Q tile, then dV^T += dO^T P reads the dO tile transposed.
+    // role 1: dP = dO V^T from the dO tile, then dK^T += Q^T dS reads the Q tile transposed.
+    tile_step(smem + (role == 0 ? cur : 2 + cur) * TILE, smem + (role == 0 ? 2 + cur : cur) * TILE,
+              smem + (cur ^ 1) * TILE, smem + (2 + (cur ^ 1)) * TILE, px, qt_n * BQ, q0, st);
   }
+  drain_tile_copies();
 
   // ---- epilogue: lane = key, registers = head-dim rows 32*db + 8*g + 4*h + e ----
   if (active && key < p.N) {

@@ -221,6 +221,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       }
     }
   }
+  drain_tile_copies();
 
   if (active && q < p.N) {
     uint16_t* dqrow = p.dq + (int64_t)b * p.dqv.sb + (int64_t)head * p.dqv.sh + (int64_t)q * p.dqv.sn + dh * DH;

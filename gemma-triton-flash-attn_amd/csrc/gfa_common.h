@@ -113,6 +113,10 @@ __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(
 // LDS traffic has drained (lgkmcnt): afterwards the whole tile is visible to every wave.
 __device__ __forceinline__ void barrier_tile() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Wait for this wave's outstanding global->LDS copies (the last, redundant prefetch of a
+// tile loop) so none lands after the workgroup's LDS has been handed to another one.
+__device__ __forceinline__ void drain_tile_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Buffer resource (V#) over one (batch, head) slice of a (B, H, N, D) tensor: raw
 // addressing (stride 0), num_records = bytes up to the end of row n_rows - 1. Buffer loads
 // whose total offset (soffset + voffset) falls past num_records return zeros, so reads of
@@ -203,8 +207,10 @@ __device__ __forceinline__ f32x16 mma_chain_lds(const char GFA_LDS* tile, const 
 }
 
 // Single-accumulator variant of mma_chain_lds (back-to-back dependent MFMAs; 16 fewer
-// live registers).
-template <bool IS_BF16, int KT, int PF>
+// live registers). With SG != 0 the scheduler is told to keep PF LDS reads in flight:
+// PF reads first, then one read after every MFMA (call it inside its own scheduling
+// region, between two sched_barrier(0)).
+template <bool IS_BF16, int KT, int PF, int SG = 0>
 __device__ __forceinline__ f32x16 mma_chain1_lds(const char GFA_LDS* tile, const int (&koff)[8], int extra,
                                                  const i16x8 (&bf)[KT]) {
   static_assert(PF <= KT, "bad chain shape");
@@ -217,6 +223,15 @@ __device__ __forceinline__ f32x16 mma_chain1_lds(const char GFA_LDS* tile, const
     const i16x8 cur = a[kk % PF];
     if (kk + PF < KT) a[kk % PF] = lds_read16(tile, koff[(kk + PF) & 7] + 256 * ((kk + PF) >> 3) + extra);
     c = mma32<IS_BF16>(cur, bf[kk], c);
+  }
+  if constexpr (SG) {
+    __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+#pragma unroll
+    for (int kk = 0; kk < KT - PF; ++kk) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
   }
   return c;
 }
@@ -231,8 +246,9 @@ __device__ __forceinline__ i16x8 tr_frag(const char GFA_LDS* tile, int offA, int
 
 // acc[db] += A(ks, db) * B[ks] over ks < NKS, db < DB, where A(ks, db) is read transposed
 // from `tile` (row block ks * 16, column block db * 32 of a D-wide row-major tile). The
-// reads run PF products ahead of the MFMAs.
-template <bool IS_BF16, int D, int DB, int NKS, int PF>
+// reads run PF products ahead of the MFMAs; SG != 0 pins that pipeline in the schedule
+// (2*PF transposing reads first, then two after every MFMA).
+template <bool IS_BF16, int D, int DB, int NKS, int PF, int SG = 0>
 __device__ __forceinline__ void mma_tr_accumulate(f32x16 (&acc)[DB], const char GFA_LDS* tile, const int (&offA)[4],
                                                   const int (&offB)[4], const i16x8 (&bop)[NKS]) {
   constexpr int N = NKS * DB;
@@ -252,6 +268,15 @@ __device__ __forceinline__ void mma_tr_accumulate(f32x16 (&acc)[DB], const char 
       a[i % PF] = tr_frag(tile, offA[db2 & 3], offB[db2 & 3], ks2 * 16 * (2 * D) + 256 * (db2 >> 2));
     }
     acc[db] = mma32<IS_BF16>(cur, bop[ks], acc[db]);
+  }
+  if constexpr (SG) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);
+#pragma unroll
+    for (int i = 0; i < N - PF; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
   }
 }
 
