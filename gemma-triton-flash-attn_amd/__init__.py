@@ -23,7 +23,7 @@ from .hf_integration import (
 from .reference import attention_gqa_ref, attention_swa_ref
 from .registry import REGISTRY, SUPPORTED_HEAD_DIMS, KernelConfig, get_config
 
-__version__ = "1.0.0"
+__version__ = "1.0.1"
 
 __all__ = [
     "attention_flash_gqa",

@@ -74,9 +74,9 @@ def _norm_window(causal: bool, slide_size: int, n: int) -> int:
 
 
 def lse_ld(n: int) -> int:
-    """Row length of the LSE / delta buffers: the backward reads whole 32-row groups
-    (GFA_LSE_LD in include/gfa.h)."""
-    return (n + 31) // 32 * 32
+    """Row length of the LSE / delta buffers: the backward reads whole query tiles of up
+    to 64 rows (GFA_LSE_LD in include/gfa.h)."""
+    return (n + 63) // 64 * 64
 
 
 def _stream(dev: torch.device) -> int:

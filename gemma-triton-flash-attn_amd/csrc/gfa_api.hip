@@ -44,7 +44,7 @@ struct Entry {
 
 constexpr Entry kRegistry[] = {
     {512, 32, 4, 32, 4, 32, 4},
-    {256, 64, 4, 32, 4, 32, 4},
+    {256, 64, 4, 32, 4, 64, 4},
 };
 
 const Entry* lookup(int d) {

@@ -219,7 +219,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
     barrier_tile();  // tile `it` landed; every wave is done with the other buffers and px
     const int q0 = qt_c * BQ;
     // Row statistics of this tile (rows q0 + sb*32 + 8g + 4h + 0..3; rows padded to a
-    // multiple of 32), issued before the prefetch so they are not queued behind it.
+    // multiple of 64), issued before the prefetch so they are not queued behind it.
     f32x4 st[SB][4];
     {
       const float* srow = stat_kv + (int64_t)r_c * p.lse_ld + q0 + 4 * h;
@@ -324,8 +324,8 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const BwdDkvParams p, i
 // Explicit instantiations of every built variant (device code and host launch stubs).
 template __global__ void bwd_dkv_kernel<512, 32, true, 4>(const BwdDkvParams);
 template __global__ void bwd_dkv_kernel<512, 32, false, 4>(const BwdDkvParams);
-template __global__ void bwd_dkv_kernel<256, 32, true, 4>(const BwdDkvParams);
-template __global__ void bwd_dkv_kernel<256, 32, false, 4>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<256, 64, true, 4>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<256, 64, false, 4>(const BwdDkvParams);
 template __global__ void dkv_reduce_kernel<true>(const BwdDkvParams, int);
 template __global__ void dkv_reduce_kernel<false>(const BwdDkvParams, int);
 
@@ -337,7 +337,7 @@ static hipError_t launch_dkv_t(const BwdDkvParams& p, hipStream_t stream) {
 
 hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, bool bf16, hipStream_t stream) {
   if (D == 512 && bq == 32) return bf16 ? launch_dkv_t<512, 32, true, 4>(p, stream) : launch_dkv_t<512, 32, false, 4>(p, stream);
-  if (D == 256 && bq == 32) return bf16 ? launch_dkv_t<256, 32, true, 4>(p, stream) : launch_dkv_t<256, 32, false, 4>(p, stream);
+  if (D == 256 && bq == 64) return bf16 ? launch_dkv_t<256, 64, true, 4>(p, stream) : launch_dkv_t<256, 64, false, 4>(p, stream);
   return hipErrorInvalidValue;
 }
 

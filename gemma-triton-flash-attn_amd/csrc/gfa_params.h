@@ -60,7 +60,7 @@ struct BwdDkvParams {
   const uint16_t* k;
   const uint16_t* v;
   const uint16_t* dout;
-  const float* lse;    // (B, Hq, lse_ld), rows padded to a multiple of 32
+  const float* lse;    // (B, Hq, lse_ld), rows padded to a multiple of 64
   const float* delta;  // same layout
   uint16_t* dk;      // written directly when q_splits == 1
   uint16_t* dv;

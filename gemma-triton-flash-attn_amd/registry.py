@@ -33,7 +33,7 @@ class KernelConfig:
 REGISTRY: dict[int, KernelConfig] = {
     512: KernelConfig(512, fwd_block_kv=32, fwd_waves=4, dq_block_kv=32, dq_waves=4, dkv_block_q=32, dkv_waves=4,
                       fwd_block_kv_options=(32,)),
-    256: KernelConfig(256, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dkv_block_q=32, dkv_waves=4,
+    256: KernelConfig(256, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dkv_block_q=64, dkv_waves=4,
                       fwd_block_kv_options=(32, 64)),
 }
 

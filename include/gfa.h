@@ -8,8 +8,8 @@
  * Tensor layout: q/o/do/dq are (B, Hq, N, D); k/v/dk/dv are (B, Hkv, N, D); every
  * tensor is addressed through its own (batch, head, row) element strides and must have
  * a unit-stride head dimension and 16-byte aligned rows. lse/delta are float32
- * (B, Hq, lse_ld) with lse_ld >= GFA_LSE_LD(N): the backward kernels read whole 32-row
- * groups, so rows N..lse_ld-1 must exist (their values are never used).
+ * (B, Hq, lse_ld) with lse_ld >= GFA_LSE_LD(N): the backward kernels read whole query
+ * tiles of up to 64 rows, so rows N..lse_ld-1 must exist (their values are never used).
  * Query head h reads KV head h / (Hq / Hkv) (contiguous groups).
  *
  * The entry points replace the reference's Triton launch sites (file:line in
@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GFA_VERSION 100 /* 1.0.0 */
+#define GFA_VERSION 101 /* 1.0.1: LSE rows padded to 64 */
 
 typedef enum {
   GFA_DTYPE_FP16 = 0,
@@ -51,7 +51,7 @@ typedef enum {
 } gfa_status;
 
 /* Smallest legal lse_ld for a sequence length. */
-#define GFA_LSE_LD(seq_len) ((((seq_len) + 31) / 32) * 32)
+#define GFA_LSE_LD(seq_len) ((((seq_len) + 63) / 64) * 64)
 
 /* gfa_bwd_args.stages bits */
 #define GFA_BWD_DQ 1  /* delta + dQ kernel */

@@ -85,7 +85,7 @@ def test_lse_and_inference_path(B, Hq, Hkv, N, D, causal, window, dtype, device)
     scale = D ** -0.5
     o, lse = _forward(q, k, v, causal, window if window < N else 0, scale, store_lse=True)
     o_ref, lse_ref = orc.forward(_np(q), _np(k), _np(v), causal, window)
-    assert lse.shape[-1] % 32 == 0 and lse.shape[-1] >= N
+    assert lse.shape[-1] % 64 == 0 and lse.shape[-1] >= N
     assert float(np.abs(_np(lse[..., :N]) - lse_ref).max()) <= 1e-2
     import gemma_triton_flash_attn_amd as gfa
 
