@@ -32,19 +32,20 @@ int ok() {
 // HEAD_DIM-keyed registry (mirrors registry.py). Replaces the reference's if/else tile
 // tables (/root/reference/flash_attn/attention.py:561-579, 1445-1451, 1498-1504,
 // 1536-1564) with MI355X tiles. Forward: one wave per 32 query rows over the full head
-// dim; dQ: wave pairs splitting the head dim, 32 query rows per pair; dK/dV: wave pairs
-// splitting the work by role (P/dV and dS/dK), 32 keys per pair. NW waves per workgroup.
+// dim; dQ: dq_split waves per 32 query rows (2 = a pair splitting the head dim, 1 = one
+// wave over the full head dim); dK/dV: wave pairs splitting the work by role (P/dV and
+// dS/dK), 32 keys per pair. NW waves per workgroup.
 // ---------------------------------------------------------------------------------
 struct Entry {
   int head_dim;
   int fwd_bkv, fwd_waves;
-  int dq_bkv, dq_waves;
+  int dq_bkv, dq_waves, dq_split;
   int dkv_bq, dkv_waves;
 };
 
 constexpr Entry kRegistry[] = {
-    {512, 32, 4, 32, 4, 32, 4},
-    {256, 64, 4, 32, 4, 64, 4},
+    {512, 32, 4, 32, 4, 2, 32, 4},
+    {256, 64, 4, 32, 4, 1, 64, 4},
 };
 
 const Entry* lookup(int d) {
@@ -128,7 +129,7 @@ int gfa_config(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len
   out->fwd_block_q = 32 * g.qbw;
   out->fwd_block_kv = e->fwd_bkv;
   out->fwd_waves = e->fwd_waves;
-  const gfa::QGrid gq = make_qgrid(batch, heads_kv, heads_q / heads_kv, seq_len, e->dq_waves / 2);
+  const gfa::QGrid gq = make_qgrid(batch, heads_kv, heads_q / heads_kv, seq_len, e->dq_waves / e->dq_split);
   out->dq_block_q = 32 * gq.qbw;
   out->dq_block_kv = e->dq_bkv;
   out->dq_waves = e->dq_waves;
@@ -257,10 +258,10 @@ int gfa_bwd(const gfa_bwd_args* a) {
   pq.scale = a->scale;
   pq.scale_log2 = scale_log2;
   pq.lse_ld = a->lse_ld;
-  pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves / 2);
+  pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves / e->dq_split);
   hipError_t err = hipSuccess;
   if (stages & GFA_BWD_DQ) {
-    err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, bf16, stream);
+    err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, e->dq_split, bf16, stream);
     if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dQ launch failed: %s", hipGetErrorString(err));
   }
   if (!(stages & GFA_BWD_DKV)) return ok();

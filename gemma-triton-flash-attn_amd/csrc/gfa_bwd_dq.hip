@@ -20,16 +20,17 @@
 
 namespace gfa {
 
-template <int D, int BKV, bool IS_BF16, int NW>
+template <int D, int BKV, bool IS_BF16, int NW, int SPLIT>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p) {
-  constexpr int DH = D / 2;
+  constexpr int DH = D / SPLIT;  // head-dim slice of one wave
   constexpr int KTH = DH / 16;
   constexpr int DBH = DH / 32;
   constexpr int SB = BKV / 32;
   constexpr int TILE = BKV * D * 2;
-  constexpr int XHALF = SB * 16 * 64 * 4;  // one f32x16 per score block per lane
-  constexpr int XCH = 2 * XHALF;          // S^T and dP^T partials
+  constexpr int XHALF = SB * 16 * 64 * 4;              // one f32x16 per score block per lane
+  constexpr int XCH = SPLIT == 2 ? 2 * XHALF : 0;     // S^T and dP^T partials of a pair
   static_assert(BKV % 32 == 0, "BKV must be a multiple of 32");
+  static_assert(SPLIT == 1 || SPLIT == 2, "one wave or a wave pair per 32 query rows");
   static_assert(DH % 128 == 0, "head dim must be 256 or 512");
 
   __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NW * XCH];
@@ -38,8 +39,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int unit = wave >> 1;
-  const int dh = wave & 1;
+  const int unit = wave / SPLIT;
+  const int dh = SPLIT == 2 ? (wave & 1) : 0;
   const int h = lane >> 5;
   const int l32 = lane & 31;
 
@@ -98,10 +99,13 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     pin_vgpr(df[kk]);
   }
   dpart += __shfl_xor(dpart, 32);
-  // Pair exchange of the two head-dim halves of delta (through the exchange area).
-  *reinterpret_cast<float GFA_LDS*>(xch + wave * XCH + lane * 4) = dpart;
-  barrier_lds();
-  const float delta = dpart + *reinterpret_cast<const float GFA_LDS*>(xch + (wave ^ 1) * XCH + lane * 4);
+  float delta = dpart;
+  if constexpr (SPLIT == 2) {
+    // Pair exchange of the two head-dim halves of delta (through the exchange area).
+    *reinterpret_cast<float GFA_LDS*>(xch + wave * XCH + lane * 4) = dpart;
+    barrier_lds();
+    delta += *reinterpret_cast<const float GFA_LDS*>(xch + (wave ^ 1) * XCH + lane * 4);
+  }
   if (active && q < p.N && dh == 0 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.lse_ld + q] = delta;
   const float lse_log2 = p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + qrow] * kLog2e;
 
@@ -134,7 +138,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   kload.init(kbase, p.kv.sn, p.N, wave, lane);
   vload.init(vbase, p.vv.sn, p.N, wave, lane);
 
-  barrier_lds();  // everyone has read the delta exchange before it is overwritten
+  if constexpr (SPLIT == 2) barrier_lds();  // everyone has read the delta exchange before it is overwritten
   if (t_lo < t_hi) {
     kload.load(t_lo * BKV, smem);
     vload.load(t_lo * BKV, smem + 2 * TILE);
@@ -163,7 +167,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
         s[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
         dp[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(vt, koff, sb * 32 * (2 * D), df);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 4 && SPLIT == 2; ++j) {
           const f32x4 vs = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
           const f32x4 vd = {dp[sb][4 * j], dp[sb][4 * j + 1], dp[sb][4 * j + 2], dp[sb][4 * j + 3]};
           *reinterpret_cast<f32x4 GFA_LDS*>(xmine + (sb * 4 + j) * 1024) = vs;
@@ -171,11 +175,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
         }
       }
     }
-    barrier_lds();
+    if constexpr (SPLIT == 2) barrier_lds();
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 4 && SPLIT == 2; ++j) {
         const f32x4 vs = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + (sb * 4 + j) * 1024);
         const f32x4 vd = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + XHALF + (sb * 4 + j) * 1024);
 #pragma unroll
@@ -239,20 +243,23 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 }
 
 // Explicit instantiations of every built variant (device code and host launch stubs).
-template __global__ void bwd_dq_kernel<512, 32, true, 4>(const BwdDqParams);
-template __global__ void bwd_dq_kernel<512, 32, false, 4>(const BwdDqParams);
-template __global__ void bwd_dq_kernel<256, 32, true, 4>(const BwdDqParams);
-template __global__ void bwd_dq_kernel<256, 32, false, 4>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<512, 32, true, 4, 2>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<512, 32, false, 4, 2>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<256, 32, true, 4, 1>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<256, 32, false, 4, 1>(const BwdDqParams);
 
-template <int D, int BKV, bool IS_BF16, int NW>
+template <int D, int BKV, bool IS_BF16, int NW, int SPLIT>
 static hipError_t launch_dq_t(const BwdDqParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
+  hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
   return hipGetLastError();
 }
 
-hipError_t launch_bwd_dq(const BwdDqParams& p, int D, int bkv, bool bf16, hipStream_t stream) {
-  if (D == 512 && bkv == 32) return bf16 ? launch_dq_t<512, 32, true, 4>(p, stream) : launch_dq_t<512, 32, false, 4>(p, stream);
-  if (D == 256 && bkv == 32) return bf16 ? launch_dq_t<256, 32, true, 4>(p, stream) : launch_dq_t<256, 32, false, 4>(p, stream);
+// Built dQ variants: D=512 on wave pairs (head-dim halves), D=256 one wave per 32 rows.
+hipError_t launch_bwd_dq(const BwdDqParams& p, int D, int bkv, int split, bool bf16, hipStream_t stream) {
+  if (D == 512 && bkv == 32 && split == 2)
+    return bf16 ? launch_dq_t<512, 32, true, 4, 2>(p, stream) : launch_dq_t<512, 32, false, 4, 2>(p, stream);
+  if (D == 256 && bkv == 32 && split == 1)
+    return bf16 ? launch_dq_t<256, 32, true, 4, 1>(p, stream) : launch_dq_t<256, 32, false, 4, 1>(p, stream);
   return hipErrorInvalidValue;
 }
 

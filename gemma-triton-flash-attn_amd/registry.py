@@ -4,9 +4,9 @@ The reference keeps its tile choices as if/else tables keyed on HEAD_DIM inside 
 launch code (/root/reference/flash_attn/attention.py:561-579 inference forward,
 1445-1451 training forward, 1498-1504 dQ, 1536-1564 dKV, 1576-1587 Q_SPLITS). Here the
 same role is one explicit table. Each entry names the tiles of the three gfx950 kernels:
-the forward runs one wave per 32 query rows over the full head dim, the dQ kernel wave
-pairs that split the head dim (32 query rows per pair), the dK/dV kernel wave pairs that
-split the work by role (32 keys per pair).
+the forward runs one wave per 32 query rows over the full head dim, the dQ kernel
+``dq_split`` waves per 32 query rows (a pair splitting the head dim at D=512, one wave at
+D=256), the dK/dV kernel wave pairs that split the work by role (32 keys per pair).
 
 The C library holds the same table (csrc/gfa_api.hip, kRegistry); ``gfa_config`` reports
 what the library will use and the tests assert the two agree.
@@ -25,15 +25,18 @@ class KernelConfig:
     fwd_waves: int      # waves per forward workgroup (pairs = waves / 2)
     dq_block_kv: int
     dq_waves: int
+    dq_split: int       # waves per 32 query rows in the dQ kernel (2: head-dim halves; 1: full)
     dkv_block_q: int    # queries per LDS tile in the dKV kernel
     dkv_waves: int
     fwd_block_kv_options: tuple = ()  # other built forward tile widths (BLOCK_KV override)
 
 
 REGISTRY: dict[int, KernelConfig] = {
-    512: KernelConfig(512, fwd_block_kv=32, fwd_waves=4, dq_block_kv=32, dq_waves=4, dkv_block_q=32, dkv_waves=4,
+    512: KernelConfig(512, fwd_block_kv=32, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=2, dkv_block_q=32,
+                      dkv_waves=4,
                       fwd_block_kv_options=(32,)),
-    256: KernelConfig(256, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dkv_block_q=64, dkv_waves=4,
+    256: KernelConfig(256, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=64,
+                      dkv_waves=4,
                       fwd_block_kv_options=(32, 64)),
 }
 
@@ -87,7 +90,7 @@ def get_config(batch: int, heads_q: int, heads_kv: int, seq_len: int, head_dim: 
     """Everything the library decides for one problem (same keys as ``gfa_config``)."""
     c = lookup(head_dim)
     fq = query_grid(batch, heads_q, heads_kv, seq_len, c.fwd_waves)
-    dq = query_grid(batch, heads_q, heads_kv, seq_len, c.dq_waves // 2)
+    dq = query_grid(batch, heads_q, heads_kv, seq_len, c.dq_waves // c.dq_split)
     return {
         "head_dim": head_dim,
         "fwd_block_q": fq["block_q"],
