@@ -33,19 +33,20 @@ int ok() {
 // tables (/root/reference/flash_attn/attention.py:561-579, 1445-1451, 1498-1504,
 // 1536-1564) with MI355X tiles. Forward: one wave per 32 query rows over the full head
 // dim; dQ: dq_split waves per 32 query rows (2 = a pair splitting the head dim, 1 = one
-// wave over the full head dim); dK/dV: wave pairs splitting the work by role (P/dV and
-// dS/dK), 32 keys per pair. NW waves per workgroup.
+// wave over the full head dim); dK/dV: dkv_roles waves per 32 keys (2 = a pair splitting
+// the work by role, P/dV and dS/dK; 1 = one wave doing all four products). NW waves per
+// workgroup.
 // ---------------------------------------------------------------------------------
 struct Entry {
   int head_dim;
   int fwd_bkv, fwd_waves;
   int dq_bkv, dq_waves, dq_split;
-  int dkv_bq, dkv_waves;
+  int dkv_bq, dkv_waves, dkv_roles;
 };
 
 constexpr Entry kRegistry[] = {
-    {512, 32, 4, 32, 4, 2, 32, 4},
-    {256, 64, 4, 32, 4, 1, 64, 4},
+    {512, 32, 4, 32, 4, 2, 32, 4, 2},
+    {256, 64, 4, 32, 4, 1, 32, 4, 1},
 };
 
 const Entry* lookup(int d) {
@@ -77,8 +78,9 @@ gfa::QGrid make_qgrid(int B, int Hkv, int R, int N, int nu) {
 }
 
 // Smallest of {1, 2, 4, 8} giving at least one workgroup per CU (256 CUs on MI355X).
-int pick_q_splits(int B, int Hkv, int N, int nw) {
-  const int keys_per_wg = 32 * (nw / 2);
+// units = 32-key units per dK/dV workgroup.
+int pick_q_splits(int B, int Hkv, int N, int units) {
+  const int keys_per_wg = 32 * units;
   const int grid = ((N + keys_per_wg - 1) / keys_per_wg) * B * Hkv;
   int qs = 1;
   while (qs < 8 && grid * qs < 256) qs *= 2;
@@ -133,10 +135,10 @@ int gfa_config(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len
   out->dq_block_q = 32 * gq.qbw;
   out->dq_block_kv = e->dq_bkv;
   out->dq_waves = e->dq_waves;
-  out->dkv_block_kv = 32 * (e->dkv_waves / 2);
+  out->dkv_block_kv = 32 * (e->dkv_waves / e->dkv_roles);
   out->dkv_block_q = e->dkv_bq;
   out->dkv_waves = e->dkv_waves;
-  out->q_splits = pick_q_splits(batch, heads_kv, seq_len, e->dkv_waves);
+  out->q_splits = pick_q_splits(batch, heads_kv, seq_len, e->dkv_waves / e->dkv_roles);
   return ok();
 }
 
@@ -194,7 +196,7 @@ size_t gfa_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, 
   (void)window;
   const Entry* e = lookup(head_dim);
   if (e == nullptr || batch <= 0 || heads_kv <= 0 || seq_len <= 0) return 0;
-  const int qs = q_splits > 0 ? q_splits : pick_q_splits(batch, heads_kv, seq_len, e->dkv_waves);
+  const int qs = q_splits > 0 ? q_splits : pick_q_splits(batch, heads_kv, seq_len, e->dkv_waves / e->dkv_roles);
   if (qs <= 1) return 0;
   return (size_t)qs * 2 * batch * heads_kv * (size_t)seq_len * head_dim * sizeof(float);
 }
@@ -219,7 +221,7 @@ int gfa_bwd(const gfa_bwd_args* a) {
   const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
   if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);
   const Entry* e = lookup(a->head_dim);
-  const int qs = a->q_splits > 0 ? a->q_splits : pick_q_splits(a->batch, a->heads_kv, a->seq_len, e->dkv_waves);
+  const int qs = a->q_splits > 0 ? a->q_splits : pick_q_splits(a->batch, a->heads_kv, a->seq_len, e->dkv_waves / e->dkv_roles);
   if (qs != 1 && qs != 2 && qs != 4 && qs != 8) return fail(GFA_ERR_INVALID_ARGUMENT, "q_splits=%d not in {1,2,4,8}", qs);
   const size_t need = gfa_bwd_workspace_size(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->causal,
                                              a->window, qs);
@@ -293,10 +295,10 @@ int gfa_bwd(const gfa_bwd_args* a) {
   pk.scale_log2 = scale_log2;
   pk.q_splits = qs;
   pk.lse_ld = a->lse_ld;
-  const int keys_per_wg = 32 * (e->dkv_waves / 2);
+  const int keys_per_wg = 32 * (e->dkv_waves / e->dkv_roles);
   pk.n_kb = (pk.N + keys_per_wg - 1) / keys_per_wg;
   pk.nblocks = pk.n_kb * pk.B * pk.Hkv * qs;
-  err = gfa::launch_bwd_dkv(pk, a->head_dim, e->dkv_bq, bf16, stream);
+  err = gfa::launch_bwd_dkv(pk, a->head_dim, e->dkv_bq, e->dkv_roles, bf16, stream);
   if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV launch failed: %s", hipGetErrorString(err));
   if (qs > 1) {
     err = gfa::launch_dkv_reduce(pk, a->head_dim, bf16, stream);

@@ -30,14 +30,19 @@
 
 namespace gfa {
 
-template <int D, int BQ, bool IS_BF16, int NW>
+// ROLES = 2: a wave pair per 32 keys, split by role (see above). ROLES = 1: one wave per
+// 32 keys does all four products (K and V rows resident, dV^T and dK^T both in AGPRs);
+// used where the head dim leaves room for both accumulators (D=256).
+template <int D, int BQ, bool IS_BF16, int NW, int ROLES>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams p) {
   constexpr int KT = D / 16;   // MFMA k-steps of the score products (full head dim)
   constexpr int DB = D / 32;   // 32-row blocks of the dV^T / dK^T accumulator
   constexpr int SB = BQ / 32;  // 32-query score blocks per tile
   constexpr int TILE = BQ * D * 2;
-  constexpr int PX = SB * 64 * 64;  // fp32 P hand-off of one pair: SB * 16 floats per lane
-  constexpr int NU = NW / 2;
+  constexpr int PX = ROLES == 2 ? SB * 64 * 64 : 0;  // fp32 P hand-off of one pair
+  constexpr int NU = NW / ROLES;                     // 32-key units per workgroup
+  constexpr int NS = 3 - ROLES;                      // stationary operands / accumulators per wave
+  static_assert(ROLES == 1 || ROLES == 2, "one wave or a role-split pair per 32 keys");
   static_assert(BQ % 32 == 0, "BQ must be a multiple of 32");
   static_assert(D % 128 == 0, "head dim must be 256 or 512");
 
@@ -46,8 +51,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int unit = wave >> 1;
-  const int role = wave & 1;  // 0: S, P and dV;  1: dP, dS and dK
+  const int unit = wave / ROLES;
+  const int role = ROLES == 2 ? (wave & 1) : 0;  // pair: 0 = S, P and dV;  1 = dP, dS and dK
   const int h = lane >> 5;
   const int l32 = lane & 31;
   char GFA_LDS* px = smem + 4 * TILE + unit * PX + lane * 16;
@@ -90,20 +95,27 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
   }
   const bool pair_full = k_last < p.N;
 
-  // ---- stationary B operand (lane = key, full head dim): K rows for role 0, V rows for role 1 ----
-  i16x8 kvf[KT];
+  // ---- stationary B operands (lane = key, full head dim) ----
+  // pair: sf[0] = K rows (role 0) or V rows (role 1);  single wave: sf[0] = K, sf[1] = V.
+  i16x8 sf[NS][KT];
   {
-    const uint16_t* base = role == 0 ? p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh + (int64_t)krow * p.kv.sn
-                                     : p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh + (int64_t)krow * p.vv.sn;
-    const uint16_t* r = base + 8 * h;
+    const uint16_t* krp = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh + (int64_t)krow * p.kv.sn + 8 * h;
+    const uint16_t* vrp = p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh + (int64_t)krow * p.vv.sn + 8 * h;
 #pragma unroll
-    for (int kk = 0; kk < KT; ++kk) kvf[kk] = *reinterpret_cast<const i16x8*>(r + 16 * kk);
+    for (int i = 0; i < NS; ++i) {
+      const uint16_t* r = (i == 0 && role == 0) ? krp : vrp;
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) sf[i][kk] = *reinterpret_cast<const i16x8*>(r + 16 * kk);
+    }
   }
 
-  // dV^T (role 0) or dK^T (role 1), 32 keys x D, in AGPRs.
-  f32x16 acc[DB];
+  // 32 keys x D fp32 accumulators in AGPRs. pair: acc[0] = dV^T (role 0) or dK^T (role 1);
+  // single wave: acc[0] = dV^T, acc[1] = dK^T.
+  f32x16 acc[NS][DB];
 #pragma unroll
-  for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
+  for (int i = 0; i < NS; ++i)
+#pragma unroll
+    for (int j = 0; j < DB; ++j) acc[i][j] = f32x16{};
 
   int roff[8];  // tile rows (A operand of S / dP): row l32, chunk 2*kk + h  (+256 * (kk >> 3))
 #pragma unroll
@@ -127,8 +139,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
   dload.init(p.dout, p.dov.sn, p.N, wave, lane);
   const uint16_t* q_kv = p.q + (int64_t)b * p.qv.sb + (int64_t)kvh * p.R * p.qv.sh;
   const uint16_t* d_kv = p.dout + (int64_t)b * p.dov.sb + (int64_t)kvh * p.R * p.dov.sh;
-  // Row statistic this wave needs: LSE for role 0 (P), delta for role 1 (dS).
-  const float* stat_kv = (role == 0 ? p.lse : p.delta) + ((int64_t)b * p.Hq + (int64_t)kvh * p.R) * p.lse_ld;
+  // Row statistics this wave needs: st[0] = LSE (role 0) or delta (role 1); single wave:
+  // st[0] = LSE, st[1] = delta.
+  const int64_t stat_off = ((int64_t)b * p.Hq + (int64_t)kvh * p.R) * p.lse_ld;
+  const float* stat_kv0 = (role == 0 ? p.lse : p.delta) + stat_off;
+  const float* stat_kv1 = p.delta + stat_off;
 
   // Iteration `it` covers head kvh*R + r of query tile qt, it = r * nqt + (qt - qt_lo);
   // (r_c, qt_c) walk it incrementally.
@@ -141,77 +156,121 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
     dload.load(qt_c * BQ, smem + 2 * TILE);
   }
 
-  // One query tile: prefetch the next tile into (qn, dn), score chain from ct, P / dS,
-  // accumulation reading tt transposed. The views are restrict-qualified: the compiler
-  // then knows that no read of ct / tt / pxr touches the prefetch targets and does not
-  // wait for the prefetch before reading the current tile.
-  auto tile_step = [&](const char GFA_LDS* __restrict__ ct, const char GFA_LDS* __restrict__ tt,
-                       char GFA_LDS* __restrict__ qn, char GFA_LDS* __restrict__ dn, char GFA_LDS* __restrict__ pxr,
-                       int row_n, int q0, const f32x4 (&st)[SB][4]) __attribute__((always_inline)) {
-    qload.load(row_n, qn);
-    dload.load(row_n, dn);
-
-    f32x16 s[SB];
-    __builtin_amdgcn_sched_barrier(0);  // the two MFMA pipelines are scheduled on their own
-#pragma unroll
-    for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(ct, roff, sb * 32 * (2 * D), kvf);
-    __builtin_amdgcn_sched_barrier(0);
-
-    if (role == 0) {
-      // P on the key lanes (rows = queries per register), masked, handed to the partner in fp32.
-      const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
-#pragma unroll
-      for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[sb][r] = fast_exp2(s[sb][r] * p.scale_log2 - st[sb][r >> 2][r & 3] * kLog2e);
-      }
-      if (need_mask) {
-#pragma unroll
-        for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int qi = q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            s[sb][r] = visible(qi, key, p.N, p.causal, p.window) ? s[sb][r] : 0.f;
-          }
-        }
-      }
-#pragma unroll
-      for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x4 v = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
-          *reinterpret_cast<f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024) = v;
-        }
-      }
-    }
-    barrier_lds();  // P of this tile is in px
-    if (role == 1) {
-      // dS = P * (dP - delta); P == 0 (masked, or underflowed) gives exactly 0, also for
-      // padding rows whose delta is not defined.
-#pragma unroll
-      for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x4 pv = *reinterpret_cast<const f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * j + e;
-            s[sb][r] = pv[e] != 0.f ? pv[e] * (s[sb][r] - st[sb][j][e]) : 0.f;
-          }
-        }
-      }
-    }
-    i16x8 pb[BQ / 16];
+  // P on the key lanes (rows = queries per register): exp2 against the row LSE, masked.
+  auto make_p = [&](f32x16 (&sc)[SB], const f32x4 (&lse)[SB][4], int q0) __attribute__((always_inline)) {
+    const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(s[sb][r]);
+      for (int r = 0; r < 16; ++r) sc[sb][r] = fast_exp2(sc[sb][r] * p.scale_log2 - lse[sb][r >> 2][r & 3] * kLog2e);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 4, 1>(acc, tt, toffA, toffB, pb);
-    __builtin_amdgcn_sched_barrier(0);
+    if (need_mask) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
+      for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qi = q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          sc[sb][r] = visible(qi, key, p.N, p.causal, p.window) ? sc[sb][r] : 0.f;
+        }
+      }
+    }
+  };
+  // dS = P * (dP - delta) in place of dP; P == 0 (masked or underflowed) gives exactly 0,
+  // also for padding rows whose delta is not defined.
+  auto make_ds = [&](f32x16& dp, const f32x4 pv4[4], const f32x4 (&del)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * j + e;
+        dp[r] = pv4[j][e] != 0.f ? pv4[j][e] * (dp[r] - del[j][e]) : 0.f;
+      }
+    }
+  };
+  auto pack = [&](const f32x16 (&v)[SB], i16x8 (&out)[BQ / 16]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) out[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(v[sb][r]);
+    }
+  };
+
+  // One query tile: prefetch the next tile into (qn, dn), score chains, P / dS,
+  // accumulations reading the tiles transposed. The views are restrict-qualified: the
+  // compiler then knows that no read of qt / dt / pxr touches the prefetch targets and
+  // does not wait for the prefetch before reading the current tile.
+  auto tile_step = [&](const char GFA_LDS* __restrict__ qt, const char GFA_LDS* __restrict__ dt,
+                       char GFA_LDS* __restrict__ qn, char GFA_LDS* __restrict__ dn, char GFA_LDS* __restrict__ pxr,
+                       int row_n, int q0, const f32x4 (&st)[NS][SB][4]) __attribute__((always_inline)) {
+    qload.load(row_n, qn);
+    dload.load(row_n, dn);
+    if constexpr (ROLES == 2) {
+      // role 0: S = Q K^T from the Q tile, then dV^T += dO^T P reads the dO tile transposed.
+      // role 1: dP = dO V^T from the dO tile, then dK^T += Q^T dS reads the Q tile transposed.
+      const char GFA_LDS* ct = role == 0 ? qt : dt;
+      const char GFA_LDS* tt = role == 0 ? dt : qt;
+      f32x16 s[SB];
+      __builtin_amdgcn_sched_barrier(0);  // the MFMA pipelines are scheduled on their own
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(ct, roff, sb * 32 * (2 * D), sf[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (role == 0) {
+        make_p(s, st[0], q0);
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const f32x4 v = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
+            *reinterpret_cast<f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024) = v;
+          }
+        }
+      }
+      barrier_lds();  // P of this tile is in px
+      if (role == 1) {
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb) {
+          f32x4 pv4[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pv4[j] = *reinterpret_cast<const f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024);
+          make_ds(s[sb], pv4, st[0][sb]);
+        }
+      }
+      i16x8 pb[BQ / 16];
+      pack(s, pb);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 4, 1>(acc[0], tt, toffA, toffB, pb);
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      // S = Q K^T, dP = dO V^T, then dV^T += dO^T P and dK^T += Q^T dS.
+      f32x16 s[SB], dp[SB];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(qt, roff, sb * 32 * (2 * D), sf[0]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) dp[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(dt, roff, sb * 32 * (2 * D), sf[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      make_p(s, st[0], q0);
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+        f32x4 pv4[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pv4[j] = f32x4{s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
+        make_ds(dp[sb], pv4, st[NS - 1][sb]);
+      }
+      i16x8 pb[BQ / 16], dsb[BQ / 16];
+      pack(s, pb);
+      pack(dp, dsb);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 4, 1>(acc[0], dt, toffA, toffB, pb);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 4, 1>(acc[NS - 1], qt, toffA, toffB, dsb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) pin_agpr(acc[i][db]);
   };
 
   for (int it = it_lo; it < it_hi; ++it) {
@@ -220,13 +279,14 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
     const int q0 = qt_c * BQ;
     // Row statistics of this tile (rows q0 + sb*32 + 8g + 4h + 0..3; rows padded to a
     // multiple of 64), issued before the prefetch so they are not queued behind it.
-    f32x4 st[SB][4];
-    {
-      const float* srow = stat_kv + (int64_t)r_c * p.lse_ld + q0 + 4 * h;
+    f32x4 st[NS][SB][4];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const float* srow = (i == 0 ? stat_kv0 : stat_kv1) + (int64_t)r_c * p.lse_ld + q0 + 4 * h;
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) st[sb][g] = *reinterpret_cast<const f32x4*>(srow + sb * 32 + 8 * g);
+        for (int g = 0; g < 4; ++g) st[i][sb][g] = *reinterpret_cast<const f32x4*>(srow + sb * 32 + 8 * g);
     }
     // Next tile; the last iteration re-fetches its own tile into the idle buffer (never
     // read) so the loop body stays branch-free.
@@ -243,42 +303,44 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
     dload.rebase(d_kv + (int64_t)r_n * p.dov.sh, p.dov.sn, p.N);
     r_c = r_n;
     qt_c = qt_n;
-    // role 0: S = Q K^T from the Q tile, then dV^T += dO^T P reads the dO tile transposed.
-    // role 1: dP = dO V^T from the dO tile, then dK^T += Q^T dS reads the Q tile transposed.
-    tile_step(smem + (role == 0 ? cur : 2 + cur) * TILE, smem + (role == 0 ? 2 + cur : cur) * TILE,
-              smem + (cur ^ 1) * TILE, smem + (2 + (cur ^ 1)) * TILE, px, qt_n * BQ, q0, st);
+    tile_step(smem + cur * TILE, smem + (2 + cur) * TILE, smem + (cur ^ 1) * TILE, smem + (2 + (cur ^ 1)) * TILE, px,
+              qt_n * BQ, q0, st);
   }
   drain_tile_copies();
 
   // ---- epilogue: lane = key, registers = head-dim rows 32*db + 8*g + 4*h + e ----
   if (active && key < p.N) {
-    const float osc = role == 0 ? 1.f : p.scale;  // dK carries the softmax scale
-    if (p.q_splits == 1) {
-      uint16_t* orow = role == 0
-                           ? p.dv + (int64_t)b * p.dvv.sb + (int64_t)kvh * p.dvv.sh + (int64_t)key * p.dvv.sn
-                           : p.dk + (int64_t)b * p.dkv.sb + (int64_t)kvh * p.dkv.sh + (int64_t)key * p.dkv.sn;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
+    for (int i = 0; i < NS; ++i) {
+      const int which = ROLES == 2 ? role : i;       // 0: dV, 1: dK
+      const float osc = which == 0 ? 1.f : p.scale;  // dK carries the softmax scale
+      if (p.q_splits == 1) {
+        uint16_t* orow = which == 0
+                             ? p.dv + (int64_t)b * p.dvv.sb + (int64_t)kvh * p.dvv.sh + (int64_t)key * p.dvv.sn
+                             : p.dk + (int64_t)b * p.dkv.sb + (int64_t)kvh * p.dkv.sh + (int64_t)key * p.dkv.sn;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          i16x4 o4;
+        for (int db = 0; db < DB; ++db) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[db][4 * g + e] * osc);
-          *reinterpret_cast<i16x4*>(orow + db * 32 + 8 * g + 4 * h) = o4;
+          for (int g = 0; g < 4; ++g) {
+            i16x4 o4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[i][db][4 * g + e] * osc);
+            *reinterpret_cast<i16x4*>(orow + db * 32 + 8 * g + 4 * h) = o4;
+          }
         }
-      }
-    } else {
-      // fp32 partials [split][dk|dv][b][kvh][key][d], dK already scaled.
-      const int64_t plane = (int64_t)p.B * p.Hkv * p.N * D;
-      const int64_t rowoff = (((int64_t)b * p.Hkv + kvh) * p.N + key) * D;
-      float* dst = p.part + (int64_t)split * 2 * plane + (role == 0 ? plane : 0) + rowoff;
+      } else {
+        // fp32 partials [split][dk|dv][b][kvh][key][d], dK already scaled.
+        const int64_t plane = (int64_t)p.B * p.Hkv * p.N * D;
+        const int64_t rowoff = (((int64_t)b * p.Hkv + kvh) * p.N + key) * D;
+        float* dst = p.part + (int64_t)split * 2 * plane + (which == 0 ? plane : 0) + rowoff;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
+        for (int db = 0; db < DB; ++db) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 v4 = {acc[db][4 * g] * osc, acc[db][4 * g + 1] * osc, acc[db][4 * g + 2] * osc,
-                            acc[db][4 * g + 3] * osc};
-          *reinterpret_cast<f32x4*>(dst + db * 32 + 8 * g + 4 * h) = v4;
+          for (int g = 0; g < 4; ++g) {
+            const f32x4 v4 = {acc[i][db][4 * g] * osc, acc[i][db][4 * g + 1] * osc, acc[i][db][4 * g + 2] * osc,
+                              acc[i][db][4 * g + 3] * osc};
+            *reinterpret_cast<f32x4*>(dst + db * 32 + 8 * g + 4 * h) = v4;
+          }
         }
       }
     }
@@ -322,22 +384,31 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const BwdDkvParams p, i
 }
 
 // Explicit instantiations of every built variant (device code and host launch stubs).
-template __global__ void bwd_dkv_kernel<512, 32, true, 4>(const BwdDkvParams);
-template __global__ void bwd_dkv_kernel<512, 32, false, 4>(const BwdDkvParams);
-template __global__ void bwd_dkv_kernel<256, 64, true, 4>(const BwdDkvParams);
-template __global__ void bwd_dkv_kernel<256, 64, false, 4>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<512, 32, true, 4, 2>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<512, 32, false, 4, 2>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<256, 32, true, 4, 1>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<256, 32, false, 4, 1>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<256, 64, true, 4, 2>(const BwdDkvParams);
+template __global__ void bwd_dkv_kernel<256, 64, false, 4, 2>(const BwdDkvParams);
 template __global__ void dkv_reduce_kernel<true>(const BwdDkvParams, int);
 template __global__ void dkv_reduce_kernel<false>(const BwdDkvParams, int);
 
-template <int D, int BQ, bool IS_BF16, int NW>
+template <int D, int BQ, bool IS_BF16, int NW, int ROLES>
 static hipError_t launch_dkv_t(const BwdDkvParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW>), dim3(p.nblocks), dim3(NW * 64), 0, stream, p);
+  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW, ROLES>), dim3(p.nblocks), dim3(NW * 64), 0, stream, p);
   return hipGetLastError();
 }
 
-hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, bool bf16, hipStream_t stream) {
-  if (D == 512 && bq == 32) return bf16 ? launch_dkv_t<512, 32, true, 4>(p, stream) : launch_dkv_t<512, 32, false, 4>(p, stream);
-  if (D == 256 && bq == 64) return bf16 ? launch_dkv_t<256, 64, true, 4>(p, stream) : launch_dkv_t<256, 64, false, 4>(p, stream);
+// Built dK/dV variants: (head dim, queries per tile, waves per 32 keys).
+hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, int roles, bool bf16, hipStream_t stream) {
+#define GFA_DKV_CASE(DD, BB, RR)                                                                   \
+  if (D == DD && bq == BB && roles == RR) {                                                        \
+    return bf16 ? launch_dkv_t<DD, BB, true, 4, RR>(p, stream) : launch_dkv_t<DD, BB, false, 4, RR>(p, stream); \
+  }
+  GFA_DKV_CASE(512, 32, 2)
+  GFA_DKV_CASE(256, 32, 1)
+  GFA_DKV_CASE(256, 64, 2)
+#undef GFA_DKV_CASE
   return hipErrorInvalidValue;
 }
 

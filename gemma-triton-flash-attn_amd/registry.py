@@ -6,7 +6,8 @@ launch code (/root/reference/flash_attn/attention.py:561-579 inference forward,
 same role is one explicit table. Each entry names the tiles of the three gfx950 kernels:
 the forward runs one wave per 32 query rows over the full head dim, the dQ kernel
 ``dq_split`` waves per 32 query rows (a pair splitting the head dim at D=512, one wave at
-D=256), the dK/dV kernel wave pairs that split the work by role (32 keys per pair).
+D=256), the dK/dV kernel ``dkv_roles`` waves per 32 keys (a role-split pair at D=512,
+one wave doing all four products at D=256).
 
 The C library holds the same table (csrc/gfa_api.hip, kRegistry); ``gfa_config`` reports
 what the library will use and the tests assert the two agree.
@@ -28,15 +29,16 @@ class KernelConfig:
     dq_split: int       # waves per 32 query rows in the dQ kernel (2: head-dim halves; 1: full)
     dkv_block_q: int    # queries per LDS tile in the dKV kernel
     dkv_waves: int
+    dkv_roles: int      # waves per 32 keys in the dKV kernel (2: role-split pair; 1: one wave)
     fwd_block_kv_options: tuple = ()  # other built forward tile widths (BLOCK_KV override)
 
 
 REGISTRY: dict[int, KernelConfig] = {
     512: KernelConfig(512, fwd_block_kv=32, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=2, dkv_block_q=32,
-                      dkv_waves=4,
+                      dkv_waves=4, dkv_roles=2,
                       fwd_block_kv_options=(32,)),
-    256: KernelConfig(256, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=64,
-                      dkv_waves=4,
+    256: KernelConfig(256, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
+                      dkv_waves=4, dkv_roles=1,
                       fwd_block_kv_options=(32, 64)),
 }
 
@@ -72,13 +74,14 @@ def query_grid(batch: int, heads_q: int, heads_kv: int, seq_len: int, units: int
             "nblocks": n_qsb * batch * heads_kv * (r // hpw)}
 
 
-def q_splits_for(batch: int, heads_kv: int, seq_len: int, waves: int) -> int:
-    """Smallest of {1, 2, 4, 8} giving at least one dKV workgroup per CU.
+def q_splits_for(batch: int, heads_kv: int, seq_len: int, units: int) -> int:
+    """Smallest of {1, 2, 4, 8} giving at least one dKV workgroup per CU (``units`` = 32-key
+    units per workgroup).
 
     Same intent as the reference's Q_SPLITS rule (attention.py:1576-1587): split each key
     block's query range only when the raw grid cannot fill the GPU.
     """
-    keys_per_wg = 32 * (waves // 2)
+    keys_per_wg = 32 * units
     grid = -(-seq_len // keys_per_wg) * batch * heads_kv
     qs = 1
     while qs < 8 and grid * qs < NUM_CUS:
@@ -99,8 +102,8 @@ def get_config(batch: int, heads_q: int, heads_kv: int, seq_len: int, head_dim: 
         "dq_block_q": dq["block_q"],
         "dq_block_kv": c.dq_block_kv,
         "dq_waves": c.dq_waves,
-        "dkv_block_kv": 32 * (c.dkv_waves // 2),
+        "dkv_block_kv": 32 * (c.dkv_waves // c.dkv_roles),
         "dkv_block_q": c.dkv_block_q,
         "dkv_waves": c.dkv_waves,
-        "q_splits": q_splits_for(batch, heads_kv, seq_len, c.dkv_waves),
+        "q_splits": q_splits_for(batch, heads_kv, seq_len, c.dkv_waves // c.dkv_roles),
     }
