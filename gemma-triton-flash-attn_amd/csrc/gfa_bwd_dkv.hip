@@ -388,8 +388,6 @@ template __global__ void bwd_dkv_kernel<512, 32, true, 4, 2>(const BwdDkvParams)
 template __global__ void bwd_dkv_kernel<512, 32, false, 4, 2>(const BwdDkvParams);
 template __global__ void bwd_dkv_kernel<256, 32, true, 4, 1>(const BwdDkvParams);
 template __global__ void bwd_dkv_kernel<256, 32, false, 4, 1>(const BwdDkvParams);
-template __global__ void bwd_dkv_kernel<256, 64, true, 4, 2>(const BwdDkvParams);
-template __global__ void bwd_dkv_kernel<256, 64, false, 4, 2>(const BwdDkvParams);
 template __global__ void dkv_reduce_kernel<true>(const BwdDkvParams, int);
 template __global__ void dkv_reduce_kernel<false>(const BwdDkvParams, int);
 
@@ -407,7 +405,6 @@ hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, int roles, bool 
   }
   GFA_DKV_CASE(512, 32, 2)
   GFA_DKV_CASE(256, 32, 1)
-  GFA_DKV_CASE(256, 64, 2)
 #undef GFA_DKV_CASE
   return hipErrorInvalidValue;
 }
