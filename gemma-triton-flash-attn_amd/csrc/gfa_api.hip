@@ -46,7 +46,7 @@ struct Entry {
 
 constexpr Entry kRegistry[] = {
     {512, 32, 4, 32, 4, 2, 32, 4, 2},
-    {256, 64, 4, 32, 4, 1, 32, 4, 1},
+    {256, 32, 4, 32, 4, 1, 32, 4, 1},
 };
 
 const Entry* lookup(int d) {

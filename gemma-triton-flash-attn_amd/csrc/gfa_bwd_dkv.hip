@@ -73,6 +73,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
   const int k_last = k0 + 31;
   const int key = k0 + l32;
   const int krow = min(key, p.N - 1);
+  const VisRange vis = queries_of_key(key, p.N, p.causal, p.window);
 
   const bool swa = p.causal && p.window > 0;
   // Query tiles the workgroup visits.
@@ -170,7 +171,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int qi = q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          sc[sb][r] = visible(qi, key, p.N, p.causal, p.window) ? sc[sb][r] : 0.f;
+          sc[sb][r] = vis.has(qi) ? sc[sb][r] : 0.f;
         }
       }
     }

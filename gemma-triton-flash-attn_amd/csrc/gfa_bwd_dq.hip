@@ -77,6 +77,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 
   const int q = q0 + l32;
   const int qrow = min(q, p.N - 1);
+  const VisRange vis = keys_of_query(q, p.N, p.causal, p.window);
   // ---- Q and dO halves (B operands), resident; delta prologue ----
   i16x8 qf[KTH], df[KTH];
   float dpart = 0.f;
@@ -202,7 +203,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          s[sb][r] = visible(q, key, p.N, p.causal, p.window) ? s[sb][r] : 0.f;
+          s[sb][r] = vis.has(key) ? s[sb][r] : 0.f;
         }
       }
     }

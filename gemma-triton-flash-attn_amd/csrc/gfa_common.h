@@ -61,14 +61,34 @@ __device__ __forceinline__ float from16(short x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Is key `key` visible to query `q`? (reference attention.py:347-355: key < N; key <= q
-// when causal; q - key < window when causal with a window). Bitwise ops only, so the
-// compiler emits compares and selects instead of per-lane branches.
-__device__ __forceinline__ bool visible(int q, int key, int n, int causal, int window) {
-  const bool in_range = (key < n) & (q < n);
-  const bool before = !causal | (key <= q);
-  const bool in_window = (window <= 0) | (q - key < window);
-  return in_range & before & in_window;
+// The visible set of one query (keys) or one key (queries) is a contiguous index range
+// (reference attention.py:347-355: key < N; key <= q when causal; q - key < window when
+// causal with a window). Built once per lane; a membership test is then one subtract and
+// one unsigned compare.
+struct VisRange {
+  int base;        // first visible index
+  unsigned width;  // last - first; an empty range has base far below any index
+  __device__ __forceinline__ bool has(int x) const { return (unsigned)(x - base) <= width; }
+};
+
+__device__ __forceinline__ VisRange make_range(int lo, int hi) {
+  const bool empty = hi < lo;
+  return VisRange{empty ? -(1 << 30) : lo, empty ? 0u : (unsigned)(hi - lo)};
+}
+
+// Keys visible to query q.
+__device__ __forceinline__ VisRange keys_of_query(int q, int n, int causal, int window) {
+  const int hi = q < n ? (causal ? q : n - 1) : -1;
+  const int lo = (causal && window > 0) ? q - window + 1 : 0;
+  return make_range(lo < 0 ? 0 : lo, hi);
+}
+
+// Queries that see key k.
+__device__ __forceinline__ VisRange queries_of_key(int k, int n, int causal, int window) {
+  const int lo = causal ? k : 0;
+  int hi = k < n ? n - 1 : -1;
+  if (causal && window > 0) hi = min(hi, k + window - 1);
+  return make_range(lo, hi);
 }
 
 // Keep a kernel-lifetime MFMA operand fragment in AGPRs. MFMA reads A/B operands from

@@ -99,6 +99,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     if (swa) all_lo = q0 + 31 - p.window + 1;
   }
   const int q = q0 + l32;
+  const VisRange vis = keys_of_query(q, p.N, p.causal, p.window);
 
   // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole kernel ----
   i16x8 qf[KT];
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          const bool ok = visible(q, key, p.N, p.causal, p.window);
+          const bool ok = vis.has(key);
           s[sb][r] = ok ? s[sb][r] : -INFINITY;
         }
       }

@@ -37,7 +37,7 @@ REGISTRY: dict[int, KernelConfig] = {
     512: KernelConfig(512, fwd_block_kv=32, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=2, dkv_block_q=32,
                       dkv_waves=4, dkv_roles=2,
                       fwd_block_kv_options=(32,)),
-    256: KernelConfig(256, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
+    256: KernelConfig(256, fwd_block_kv=32, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
                       dkv_waves=4, dkv_roles=1,
                       fwd_block_kv_options=(32, 64)),
 }
