@@ -198,8 +198,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
         pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
       }
     }
-    // O^T += V^T P^T as its own scheduling region with a fixed read-ahead pipeline.
-    __builtin_amdgcn_sched_barrier(0);
+    // O^T += V^T P^T with a fixed read-ahead pipeline; the softmax above shares the
+    // scheduling region, so its VALU work can fill the MFMA shadow.
     mma_tr_accumulate<IS_BF16, D, DB, BKV / 16, 2, 1>(acc, vt, voffA, voffB, pb);
     __builtin_amdgcn_sched_barrier(0);
     // Keep O^T in AGPRs across iterations (the VGPRs hold Q and the working set).
