@@ -60,6 +60,8 @@ SMALL = [
     (1, 8, 8, 33, 256, False, 0, torch.float16),
     (1, 4, 4, 1, 512, True, 0, torch.bfloat16),     # N = 1
     (1, 6, 3, 31, 256, True, 0, torch.bfloat16),    # odd group size
+    (2, 8, 2, 160, 512, True, 0, torch.float16),    # batch > 1 at D=512
+    (1, 8, 1, 130, 512, True, 40, torch.bfloat16),  # sliding window at D=512
 ]
 
 
@@ -133,15 +135,16 @@ def test_deterministic(device):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("qs", [2, 4, 8])
-def test_q_splits_match(qs, device):
-    """Q-split fp32 partials + reduction agree with the single-split kernel."""
+@pytest.mark.parametrize("qs,D", [(2, 256), (4, 256), (8, 256), (2, 512), (8, 512)])
+def test_q_splits_match(qs, D, device):
+    """Q-split fp32 partials + reduction agree with the single-split kernel (both dK/dV
+    kernel forms: one wave per 32 keys at D=256, role-split pairs at D=512)."""
     from gemma_triton_flash_attn_amd.attention import _backward, _forward
 
-    q, k, v, do = make_inputs(1, 8, 1, 256, 256, torch.bfloat16, device, seed=5)
-    o, lse = _forward(q, k, v, True, 0, 256 ** -0.5, store_lse=True)
-    ref = _backward(q, k, v, o, lse, do, True, 0, 256 ** -0.5, q_splits=1)
-    got = _backward(q, k, v, o, lse, do, True, 0, 256 ** -0.5, q_splits=qs)
+    q, k, v, do = make_inputs(1, 8, 1, 256, D, torch.bfloat16, device, seed=5)
+    o, lse = _forward(q, k, v, True, 0, D ** -0.5, store_lse=True)
+    ref = _backward(q, k, v, o, lse, do, True, 0, D ** -0.5, q_splits=1)
+    got = _backward(q, k, v, o, lse, do, True, 0, D ** -0.5, q_splits=qs)
     torch.cuda.synchronize()
     assert torch.equal(ref[0], got[0])  # dQ does not depend on the split
     for a, b in zip(ref[1:3], got[1:3]):
@@ -180,3 +183,17 @@ def test_late_large_scores(dtype, jump, device):
         assert torch.isfinite(got).all()
         if dtype == torch.float16:
             assert _rel(_np(got), ref) <= GRAD_TOL
+
+
+@pytest.mark.parametrize("block_kv", [32, 64])
+def test_block_kv_override_d256(block_kv, device):
+    """attention_flash_gqa's BLOCK_KV picks one of the built D=256 forward tiles; every
+    choice matches the oracle and they agree with each other closely."""
+    import gemma_triton_flash_attn_amd as gfa
+
+    q, k, v, _ = make_inputs(1, 4, 2, 150, 256, torch.bfloat16, device, seed=21)
+    o = gfa.attention_flash_gqa(q, k, v, causal=True, slide_size=50, BLOCK_KV=block_kv)
+    o_def = gfa.attention_flash_gqa(q, k, v, causal=True, slide_size=50)
+    o_ref, _ = orc.forward(_np(q), _np(k), _np(v), True, 50)
+    assert float(np.abs(_np(o) - o_ref).max()) <= O_TOL[torch.bfloat16]
+    assert float((o.float() - o_def.float()).abs().max()) <= 1e-2
