@@ -99,7 +99,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     pin_vgpr(qf[kk]);
     pin_vgpr(df[kk]);
   }
-  dpart += __shfl_xor(dpart, 32);
+  dpart = halves_sum(dpart);
   float delta = dpart;
   if constexpr (SPLIT == 2) {
     // Pair exchange of the two head-dim halves of delta (through the exchange area).

@@ -61,6 +61,18 @@ __device__ __forceinline__ float from16(short x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Combine a value with the one held by the lane 32 apart (the other half of a 32-row
+// fragment): v_permlane32_swap exchanges the wave halves in registers, without an LDS
+// round trip. Both lanes of a pair get the same result.
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // The visible set of one query (keys) or one key (queries) is a contiguous index range
 // (reference attention.py:347-355: key < N; key <= q when causal; q - key < window when
 // causal with a window). Built once per lane; a membership test is then one subtract and

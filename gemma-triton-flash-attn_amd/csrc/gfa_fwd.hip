@@ -183,7 +183,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
         mt = fmaxf(mt, s[sb][r]);
       }
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    mt = halves_max(mt);
     // First tile with a visible key fixes m_ref; acc and l are still zero for this row.
     m_ref = (m_ref == kNegBig && mt > kNegBig) ? mt : m_ref;
     ovf = ovf || (mt > m_ref + kMargin);
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   }
 
   // ---- epilogue: normalise, store O and LSE ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = halves_sum(l_run);
   if (active && q < p.N) {
     const float inv = 1.0f / l_tot;
     uint16_t* orow = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh + (int64_t)q * p.ov.sn;
