@@ -203,8 +203,9 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
   auto tile_step = [&](const char GFA_LDS* __restrict__ qt, const char GFA_LDS* __restrict__ dt,
                        char GFA_LDS* __restrict__ qn, char GFA_LDS* __restrict__ dn, char GFA_LDS* __restrict__ pxr,
                        int row_n, int q0, const f32x4 (&st)[NS][SB][4]) __attribute__((always_inline)) {
-    qload.load(row_n, qn);
-    dload.load(row_n, dn);
+    // The copies of the next tile are spread over the score chains, one every few MFMAs (a
+    // run of copy issues would hold up the in-order MFMA stream).
+    constexpr int NI = TileLoader<D, BQ, NW>::NI;  // copy instructions per tile and wave
     if constexpr (ROLES == 2) {
       // role 0: S = Q K^T from the Q tile, then dV^T += dO^T P reads the dO tile transposed.
       // role 1: dP = dO V^T from the dO tile, then dK^T += Q^T dS reads the Q tile transposed.
@@ -213,7 +214,19 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
       f32x16 s[SB];
       __builtin_amdgcn_sched_barrier(0);  // the MFMA pipelines are scheduled on their own
 #pragma unroll
-      for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(ct, roff, sb * 32 * (2 * D), sf[0]);
+      for (int sb = 0; sb < SB; ++sb) {
+        if (sb == 0) {
+          s[sb] = mma_chain1_lds_ld<IS_BF16, KT, 4, 2 * NI>(ct, roff, 0, sf[0], [&](int i) {
+            if (i < NI) {
+              qload.load_part(i, row_n, qn);
+            } else {
+              dload.load_part(i - NI, row_n, dn);
+            }
+          });
+        } else {
+          s[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(ct, roff, sb * 32 * (2 * D), sf[0]);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
       if (role == 0) {
         make_p(s, st[0], q0);
@@ -246,10 +259,22 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
       f32x16 s[SB], dp[SB];
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(qt, roff, sb * 32 * (2 * D), sf[0]);
+      for (int sb = 0; sb < SB; ++sb) {
+        if (sb == 0) {
+          s[sb] = mma_chain1_lds_ld<IS_BF16, KT, 4, NI>(qt, roff, 0, sf[0], [&](int i) { qload.load_part(i, row_n, qn); });
+        } else {
+          s[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(qt, roff, sb * 32 * (2 * D), sf[0]);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int sb = 0; sb < SB; ++sb) dp[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(dt, roff, sb * 32 * (2 * D), sf[1]);
+      for (int sb = 0; sb < SB; ++sb) {
+        if (sb == 0) {
+          dp[sb] = mma_chain1_lds_ld<IS_BF16, KT, 4, NI>(dt, roff, 0, sf[1], [&](int i) { dload.load_part(i, row_n, dn); });
+        } else {
+          dp[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(dt, roff, sb * 32 * (2 * D), sf[1]);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
       make_p(s, st[0], q0);
 #pragma unroll

@@ -13,7 +13,8 @@
 // over its half, and swaps them with the partner through LDS. P^T and dS^T then live on
 // the query lanes with per-lane LSE and delta, and dQ^T[half] += K^T[half] dS^T reads its
 // A operand with ds_read_b64_tr_b16 from the same row-major K tile that fed S^T. K and V
-// tiles are double-buffered in LDS via buffer loads that write LDS directly.
+// tiles are double-buffered in LDS via buffer loads that write LDS directly; the copies of
+// the next tile are spread over the S^T and dP^T chains.
 #include "gfa_common.h"
 #include "gfa_params.h"
 #include "gfa_launch.h"
@@ -33,9 +34,20 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   static_assert(SPLIT == 1 || SPLIT == 2, "one wave or a wave pair per 32 query rows");
   static_assert(DH % 128 == 0, "head dim must be 256 or 512");
 
-  __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NW * XCH];
-  char GFA_LDS* smem = (char GFA_LDS*)smem_raw;
-  char GFA_LDS* xch = smem + 4 * TILE;
+  // Four distinct LDS tile objects (not one array indexed by a buffer id): with the loop
+  // unrolled by two every access names its buffer statically, so the compiler's wait
+  // insertion can tell the in-flight copies (into the other buffers) from the tile being
+  // read and does not stall on them.
+  __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
+  __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
+  __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
+  __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
+  __shared__ __attribute__((aligned(1024))) char xch_raw[NW * XCH > 0 ? NW * XCH : 16];
+  char GFA_LDS* const K0 = (char GFA_LDS*)k_lds0;
+  char GFA_LDS* const K1 = (char GFA_LDS*)k_lds1;
+  char GFA_LDS* const V0 = (char GFA_LDS*)v_lds0;
+  char GFA_LDS* const V1 = (char GFA_LDS*)v_lds1;
+  char GFA_LDS* xch = (char GFA_LDS*)xch_raw;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -65,7 +77,9 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     if (swa) k_lo = max(0, wg_q_lo - p.window + 1);
   }
   const int t_lo = k_lo / BKV;
-  const int t_hi = (k_hi + BKV - 1) / BKV;
+  // Even tile count (the loop is unrolled by two): an odd range gets one extra tile past
+  // the workgroup's keys, which is fully masked (dS = 0; zero-filled past the sequence end).
+  const int t_hi = t_lo + ((((k_hi + BKV - 1) / BKV) - t_lo + 1) & ~1);
 
   const bool active = q0 < p.N;
   const int q_last = q0 + 31;
@@ -140,53 +154,54 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   vload.init(vbase, p.vv.sn, p.N, wave, lane);
 
   if constexpr (SPLIT == 2) barrier_lds();  // everyone has read the delta exchange before it is overwritten
-  if (t_lo < t_hi) {
-    kload.load(t_lo * BKV, smem);
-    vload.load(t_lo * BKV, smem + 2 * TILE);
-  }
 
-  for (int t = t_lo; t < t_hi; ++t) {
-    const int cur = (t - t_lo) & 1;
-    barrier_tile();
-    {
-      // Prefetch the next tile; the last iteration re-fetches its own tile into the idle
-      // buffer (never read) so the loop body stays branch-free.
-      const int tn = min(t + 1, t_hi - 1);
-      kload.load(tn * BKV, smem + (cur ^ 1) * TILE);
-      vload.load(tn * BKV, smem + (2 + (cur ^ 1)) * TILE);
-    }
+  // One key tile: wait for it, then S^T = K Q^T and dP^T = V dO^T with the copies of tile
+  // t+1 into the other buffers spread over the two chains (a run of copy issues would hold
+  // up the in-order MFMA stream), dS^T, and dQ^T += K^T dS^T.
+  constexpr int NI = TileLoader<D, BKV, NW>::NI;  // copy instructions per tile and wave
+  auto step = [&](int t, const char GFA_LDS* kt, const char GFA_LDS* vt, char GFA_LDS* kn,
+                  char GFA_LDS* vn) __attribute__((always_inline)) {
+    barrier_tile();  // tile t landed; every wave is done reading the other buffers
+    // The last step re-fetches its own tile into the idle buffers (never read) so the
+    // body stays branch-free.
+    const int rn = min(t + 1, t_hi - 1) * BKV;
     const int k0 = t * BKV;
-    const char GFA_LDS* kt = smem + cur * TILE;
-    const char GFA_LDS* vt = smem + (2 + cur) * TILE;
 
+    // No per-pair skip: a tile this pair cannot see is fully masked below, and the
+    // straight-line body keeps the accumulators resident in registers.
     f32x16 s[SB], dp[SB];
-    {
-      // No per-pair skip: a tile this pair cannot see is fully masked below, and the
-      // straight-line body keeps the accumulators resident in registers.
+    s[0] = mma_chain1_lds_ld<IS_BF16, KTH, 4, NI>(kt, koff, 0, qf, [&](int i) { kload.load_part(i, rn, kn); });
+    __builtin_amdgcn_sched_barrier(0);
+    dp[0] = mma_chain1_lds_ld<IS_BF16, KTH, 4, NI>(vt, koff, 0, df, [&](int i) { vload.load_part(i, rn, vn); });
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int sb = 1; sb < SB; ++sb) {
+      s[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
+      dp[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(vt, koff, sb * 32 * (2 * D), df);
+    }
+    if constexpr (SPLIT == 2) {
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
-        s[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
-        dp[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(vt, koff, sb * 32 * (2 * D), df);
 #pragma unroll
-        for (int j = 0; j < 4 && SPLIT == 2; ++j) {
+        for (int j = 0; j < 4; ++j) {
           const f32x4 vs = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
           const f32x4 vd = {dp[sb][4 * j], dp[sb][4 * j + 1], dp[sb][4 * j + 2], dp[sb][4 * j + 3]};
           *reinterpret_cast<f32x4 GFA_LDS*>(xmine + (sb * 4 + j) * 1024) = vs;
           *reinterpret_cast<f32x4 GFA_LDS*>(xmine + XHALF + (sb * 4 + j) * 1024) = vd;
         }
       }
-    }
-    if constexpr (SPLIT == 2) barrier_lds();
+      barrier_lds();
 #pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
+      for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-      for (int j = 0; j < 4 && SPLIT == 2; ++j) {
-        const f32x4 vs = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + (sb * 4 + j) * 1024);
-        const f32x4 vd = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + XHALF + (sb * 4 + j) * 1024);
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 vs = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + (sb * 4 + j) * 1024);
+          const f32x4 vd = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + XHALF + (sb * 4 + j) * 1024);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s[sb][4 * j + e] = s[sb][4 * j + e] + vs[e];
-          dp[sb][4 * j + e] = dp[sb][4 * j + e] + vd[e];
+          for (int e = 0; e < 4; ++e) {
+            s[sb][4 * j + e] = s[sb][4 * j + e] + vs[e];
+            dp[sb][4 * j + e] = dp[sb][4 * j + e] + vd[e];
+          }
         }
       }
     }
@@ -213,18 +228,22 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 #pragma unroll
       for (int r = 0; r < 16; ++r) dsb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(s[sb][r]);
     }
+    // dQ^T[half] += K^T[half] dS^T, A operand read transposed from the K tile.
+    mma_tr_accumulate<IS_BF16, D, DBH, BKV / 16, 2, 1>(acc, kt, toffA, toffB, dsb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int db = 0; db < DBH; ++db) pin_agpr(acc[db]);
+  };
 
-#pragma unroll
-    for (int ks = 0; ks < BKV / 16; ++ks) {
-#pragma unroll
-      for (int db = 0; db < DBH; ++db) {
-        const int imm = ks * 16 * (2 * D) + 256 * (db >> 2);
-        const i16x4 lo = lds_read_tr(kt, toffA[db & 3] + imm);
-        const i16x4 hi = lds_read_tr(kt, toffB[db & 3] + imm);
-        const i16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        acc[db] = mma32<IS_BF16>(a, dsb[ks], acc[db]);
-      }
-    }
+  if (t_lo < t_hi) {
+    kload.load(t_lo * BKV, K0);
+    vload.load(t_lo * BKV, V0);
+  }
+  for (int t = t_lo; t < t_hi; t += 2) {
+    step(t, K0, V0, K1, V1);
+    __builtin_amdgcn_sched_barrier(0);
+    step(t + 1, K1, V1, K0, V0);
+    __builtin_amdgcn_sched_barrier(0);
   }
   drain_tile_copies();
 

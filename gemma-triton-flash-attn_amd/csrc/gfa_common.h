@@ -203,6 +203,13 @@ struct TileLoader {
     rsrc = slice_rsrc(base, row_stride, n_rows, D);
   }
 
+  // Instruction i (< NI) of load(): lets a caller spread a tile copy over other work.
+  __device__ __forceinline__ void load_part(int i, int row0, char GFA_LDS* tile) const {
+    const int grp = i * NW + wave;
+    const unsigned soff = (unsigned)(row0 + grp * RPI) * stride_b;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void GFA_LDS*)(tile + grp * 1024), 16, voff[i % NV], soff, 0, 0);
+  }
+
   __device__ __forceinline__ void load(int row0, char GFA_LDS* tile) const {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -264,6 +271,36 @@ __device__ __forceinline__ f32x16 mma_chain1_lds(const char GFA_LDS* tile, const
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
+  }
+  return c;
+}
+
+// mma_chain1_lds with NL tile-copy instructions ld(0..NL-1) spread over the chain, one after
+// every KT / NL MFMAs. A wave issues in order and the copies of all its workgroup's waves
+// share the CU's texture path (each copy instruction moves 1 KB), so a run of copy issues
+// holds up the MFMAs behind it; one copy every few MFMAs keeps the MFMA stream moving.
+template <bool IS_BF16, int KT, int PF, int NL, typename LD>
+__device__ __forceinline__ f32x16 mma_chain1_lds_ld(const char GFA_LDS* tile, const int (&koff)[8], int extra,
+                                                    const i16x8 (&bf)[KT], LD&& ld) {
+  static_assert(PF <= KT && NL >= 1 && KT % NL == 0, "bad chain shape");
+  constexpr int EV = KT / NL;
+  f32x16 c = f32x16{};
+  i16x8 a[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, koff[i & 7] + 256 * (i >> 3) + extra);
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const i16x8 cur = a[kk % PF];
+    if (kk + PF < KT) a[kk % PF] = lds_read16(tile, koff[(kk + PF) & 7] + 256 * ((kk + PF) >> 3) + extra);
+    c = mma32<IS_BF16>(cur, bf[kk], c);
+    if (kk % EV == 0) ld(kk / EV);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (kk + PF < KT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if (kk % EV == 0) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
   }
   return c;
 }

@@ -17,9 +17,11 @@
 //    ds_read_b64_tr_b16 from the row-major V tile. O^T (32 x D fp32) lives in AGPRs.
 //  * K/V tiles move HBM -> LDS with buffer loads that write LDS directly (no VGPR
 //    staging; the buffer range check turns rows past the sequence end into zeros), double
-//    buffered, XOR-swizzled so both LDS read patterns are bank-conflict free. The tile loop body is
-//    straight-line code (no per-wave skips, branch-free prefetch) so the accumulators
-//    never leave the AGPRs.
+//    buffered, XOR-swizzled so both LDS read patterns are bank-conflict free. The copy of
+//    the next tile is spread over the S^T chain, one copy instruction every two MFMAs: the
+//    copies of all waves share the CU's texture path, and a run of them would hold up the
+//    in-order MFMA stream. The tile loop body is straight-line code (no per-wave skips,
+//    branch-free prefetch) so the accumulators never leave the AGPRs.
 //  * Softmax uses a fixed per-row reference max instead of a running rescale: the first
 //    tile in which a row sees a key sets m_ref, later tiles use p = exp2(s - m_ref), so the
 //    loop never rescales O. If any row later meets a score above m_ref + kMargin (P could
@@ -145,22 +147,27 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   // One pass over the workgroup's key tiles. Written once, expanded twice below: the
   // rare redo pass is a second straight-line copy rather than an outer loop, which keeps
   // the accumulators' live ranges simple enough to stay in AGPRs.
-  // One key tile: wait for it, prefetch the next one into the other buffers, then
-  // S^T = K Q^T, softmax against the fixed reference max, O^T += V^T P^T.
+  // One key tile: wait for it, then S^T = K Q^T with the copy of tile t+1 into the other
+  // buffers spread over the chain, softmax against the fixed reference max, O^T += V^T P^T.
+  constexpr int NI = TileLoader<D, BKV, NW>::NI;  // copy instructions per tile and wave
   auto step = [&](int t, const char GFA_LDS* kt, const char GFA_LDS* vt, char GFA_LDS* kn,
                   char GFA_LDS* vn) __attribute__((always_inline)) {
     barrier_tile();  // tile t landed; every wave is done reading the other buffers
-    {
-      // The last step re-fetches its own tile into the idle buffers (never read) so the
-      // body stays branch-free.
-      const int tn = min(t + 1, t_hi - 1);
-      kload.load(tn * BKV, kn);
-      vload.load(tn * BKV, vn);
-    }
+    // The last step re-fetches its own tile into the idle buffers (never read) so the
+    // body stays branch-free.
+    const int rn = min(t + 1, t_hi - 1) * BKV;
     const int k0 = t * BKV;
     f32x16 s[SB];
+    s[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, 2 * NI>(kt, koff, 0, qf, [&](int i) {
+      if (i < NI) {
+        kload.load_part(i, rn, kn);
+      } else {
+        vload.load_part(i - NI, rn, vn);
+      }
+    });
 #pragma unroll
-    for (int sb = 0; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4>(kt, koff, sb * 32 * (2 * D), qf);
+    for (int sb = 1; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4>(kt, koff, sb * 32 * (2 * D), qf);
+    __builtin_amdgcn_sched_barrier(0);
 
     const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
     if (need_mask) {
