@@ -144,9 +144,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   float m_seen = kNegBig;  // exact running max (only consulted for the redo pass)
   float l_run = 0.f;       // partial row sum over this lane half's keys
   bool ovf = false;
-  // One pass over the workgroup's key tiles. Written once, expanded twice below: the
-  // rare redo pass is a second straight-line copy rather than an outer loop, which keeps
-  // the accumulators' live ranges simple enough to stay in AGPRs.
   // One key tile: wait for it, then S^T = K Q^T with the copy of tile t+1 into the other
   // buffers spread over the chain, softmax against the fixed reference max, O^T += V^T P^T.
   constexpr int NI = TileLoader<D, BKV, NW>::NI;  // copy instructions per tile and wave
