@@ -6,6 +6,9 @@ computed by hand-written HIP kernels behind a C ABI (include/gfa.h, libgfa.so):
     attention_flash_gqa(q, k, v, causal=False, slide_size=0) -> out      inference forward
     flash_attn_gqa_train(q, k, v, causal=False, slide_size=0) -> out     autograd forward
     FlashAttnGQAFunction                                                 the autograd function
+    flash_attn_gqa_op(q, k, v, causal=False, slide_size=0) -> out        same, as torch.library
+                                                                         ops gfa::attn_fwd/bwd
+                                                                         (torch.compile-able)
     attention(q, k, v)                                                   non-causal MHA
     attention_gqa_ref / attention_swa_ref                                torch math references
     register_triton_attention(name="triton_gqa"), triton_gqa_attention   HF integration
@@ -14,6 +17,7 @@ computed by hand-written HIP kernels behind a C ABI (include/gfa.h, libgfa.so):
 q: (B, N_Q_HEADS, N, D), k/v: (B, N_KV_HEADS, N, D), fp16/bf16, D in {256, 512}.
 """
 from .attention import FlashAttnGQAFunction, attention, attention_flash_gqa, flash_attn_gqa_train
+from .ops import flash_attn_gqa_op
 from .hf_integration import (
     patch_gemma4_shared_kv_states_for_fsdp2,
     patch_transformers_5_5_4_flash_attn_key,
@@ -29,6 +33,7 @@ __all__ = [
     "attention_flash_gqa",
     "flash_attn_gqa_train",
     "FlashAttnGQAFunction",
+    "flash_attn_gqa_op",
     "attention_gqa_ref",
     "attention_swa_ref",
     "attention",

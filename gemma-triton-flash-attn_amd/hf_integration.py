@@ -6,18 +6,22 @@ adds ``triton_gqa_attention`` to transformers' attention registry under ``name``
 then ``model.config._attn_implementation = name`` routes every layer through the gfx950
 kernels.
 
-Differences from the reference adapter, both removing a full-size copy per call:
+Differences from the reference adapter:
   * ``scaling`` is passed to the kernels natively instead of pre-multiplying q
-    (reference 55-58);
+    (reference 55-58), which removes a full-size copy per call;
   * the output is allocated with q's strides, so for transformers' transposed
     (B, H, N, D) views of (B, N, H, D) projections the final ``transpose(1, 2)`` is
-    already contiguous and ``.contiguous()`` does not copy (reference 75).
+    already contiguous and ``.contiguous()`` does not copy (reference 75);
+  * the call goes through the registered ``gfa::attn_fwd`` op (``ops.py``), so a model
+    under ``torch.compile`` keeps one graph across its attention layers. The op launches on
+    its tensors' device itself, which replaces the reference's ``torch.cuda.device`` guard
+    (68-74).
 """
 from __future__ import annotations
 
 import torch
 
-from .attention import flash_attn_gqa_train
+from .ops import flash_attn_gqa_op
 
 
 def triton_gqa_attention(module, query, key, value, attention_mask, dropout: float = 0.0,
@@ -36,9 +40,7 @@ def triton_gqa_attention(module, query, key, value, attention_mask, dropout: flo
     scale = scaling if scaling is not None else module.head_dim ** -0.5
     slide = int(sliding_window) if sliding_window else 0
     is_causal = getattr(module, "is_causal", True)
-    # Launch on the tensors' device (accelerate may place layers on other GPUs).
-    with torch.cuda.device(query.device):
-        out = flash_attn_gqa_train(query, key, value, causal=is_causal, slide_size=slide, scale=scale)
+    out = flash_attn_gqa_op(query, key, value, causal=is_causal, slide_size=slide, scale=scale)
     return out.transpose(1, 2).contiguous(), None
 
 

@@ -1,0 +1,82 @@
+"""torch.library registration of the engine: ``gfa::attn_fwd`` and ``gfa::attn_bwd``.
+
+The reference's training entry point is an ``autograd.Function`` whose forward and backward
+launch Triton kernels (/root/reference/flash_attn/attention.py:1433-1635). The same calls
+here go through ctypes into libgfa.so, which ``torch.compile`` cannot trace, so a compiled
+model would break its graph at every attention layer. Registered as custom ops (with
+shape-only "fake" implementations and an autograd formula), the engine is one opaque node
+in the graph: ``flash_attn_gqa_op`` under ``torch.compile(fullgraph=True)`` traces
+without a break, and the captured graph can be replayed with HIP graphs. The kernels and
+numerics are the ones ``flash_attn_gqa_train`` runs.
+
+``attn_fwd(q, k, v, causal, window, scale) -> (O, LSE)``: ``window`` is already normalised
+(0 = none; only honoured when causal), LSE is fp32 (B, Hq, lse_ld(N)) and not
+differentiable. ``attn_bwd(q, k, v, O, LSE, dO, causal, window, scale) -> (dQ, dK, dV)``.
+"""
+from __future__ import annotations
+
+import torch
+
+from .attention import _backward, _check_inputs, _default_scale, _forward, _norm_window, _prep, lse_ld
+
+
+def _out_like(t: torch.Tensor) -> torch.Tensor:
+    """Output buffer with t's layout, or contiguous when that layout breaks the ABI's row
+    rules (the same choice the eager path makes; fake tensors have no data pointer, and real
+    allocations are always 16-byte aligned, so only the strides are checked)."""
+    o = torch.empty_like(t)
+    s = o.stride()
+    if s[3] != 1 or any(x % 8 for x in s[:3]):
+        o = torch.empty(t.shape, dtype=t.dtype, device=t.device)
+    return o
+
+
+@torch.library.custom_op("gfa::attn_fwd", mutates_args=(), device_types="cuda")
+def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, window: int,
+             scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    o, lse = _forward(q, k, v, causal, window, scale, store_lse=True)
+    return o, lse
+
+
+@attn_fwd.register_fake
+def _attn_fwd_fake(q, k, v, causal, window, scale):
+    B, Hq, N, _ = q.shape
+    return _out_like(q), q.new_empty((B, Hq, lse_ld(N)), dtype=torch.float32)
+
+
+@torch.library.custom_op("gfa::attn_bwd", mutates_args=(), device_types="cuda")
+def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, lse: torch.Tensor,
+             do: torch.Tensor, causal: bool, window: int, scale: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    dq, dk, dv, _ = _backward(_prep(q), _prep(k), _prep(v), o, lse, do, causal, window, scale)
+    return dq, dk, dv
+
+
+@attn_bwd.register_fake
+def _attn_bwd_fake(q, k, v, o, lse, do, causal, window, scale):
+    return _out_like(q), _out_like(k), _out_like(v)
+
+
+def _setup_context(ctx, inputs, output):
+    q, k, v, causal, window, scale = inputs
+    o, lse = output
+    ctx.save_for_backward(q, k, v, o, lse)
+    ctx.causal, ctx.window, ctx.scale = causal, window, scale
+    ctx.mark_non_differentiable(lse)
+
+
+def _attn_fwd_backward(ctx, do, _dlse):
+    q, k, v, o, lse = ctx.saved_tensors
+    dq, dk, dv = attn_bwd(q, k, v, o, lse, do, ctx.causal, ctx.window, ctx.scale)
+    return dq, dk, dv, None, None, None
+
+
+attn_fwd.register_autograd(_attn_fwd_backward, setup_context=_setup_context)
+
+
+def flash_attn_gqa_op(q, k, v, causal=False, slide_size=0, *, scale=None):
+    """``flash_attn_gqa_train`` through the registered op: same arguments, kernels and
+    results, and traceable by ``torch.compile`` (no graph break at the attention call)."""
+    _check_inputs(q, k, v)
+    window = _norm_window(causal, slide_size, q.shape[2])
+    o, _ = torch.ops.gfa.attn_fwd(q, k, v, bool(causal), int(window), _default_scale(q.shape[3], scale))
+    return o

@@ -1,0 +1,60 @@
+"""The torch.library ops (ops.py) on the GPU: torch.library.opcheck over the registration,
+bitwise agreement with the autograd.Function path (same kernels), and torch.compile with
+fullgraph=True through forward and backward (no graph break at the attention call)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import gemma_triton_flash_attn_amd  # noqa: F401  (registers gfa::attn_fwd / gfa::attn_bwd)
+from conftest import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+CASES = [(1, 8, 1, 128, 512, True, 0), (1, 4, 2, 96, 256, True, 40), (1, 2, 2, 64, 256, False, 0)]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,causal,window", CASES)
+def test_opcheck(B, Hq, Hkv, N, D, causal, window, device):
+    print(f"case opcheck B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal} window={window}", flush=True)
+    q, k, v, _ = make_inputs(B, Hq, Hkv, N, D, torch.bfloat16, device, seed=3)
+    q, k, v = (t.requires_grad_(True) for t in (q, k, v))
+    torch.library.opcheck(torch.ops.gfa.attn_fwd, (q, k, v, causal, window, D ** -0.5),
+                          test_utils=("test_schema", "test_autograd_registration", "test_faketensor"))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,causal,window", CASES)
+def test_op_matches_function_bitwise(B, Hq, Hkv, N, D, causal, window, device):
+    import gemma_triton_flash_attn_amd as gfa
+
+    print(f"case op-vs-function B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal} window={window}", flush=True)
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, torch.bfloat16, device, seed=4)
+    outs = []
+    for fn in (gfa.flash_attn_gqa_train, gfa.flash_attn_gqa_op):
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+        o = fn(qq, kk, vv, causal=causal, slide_size=window)
+        o.backward(do)
+        outs.append((o.detach(), qq.grad, kk.grad, vv.grad))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_compile_fullgraph_forward_backward(device):
+    import gemma_triton_flash_attn_amd as gfa
+
+    print("case torch.compile fullgraph aot_eager D=256 window=48", flush=True)
+    q, k, v, do = make_inputs(1, 8, 2, 160, 256, torch.bfloat16, device, seed=5, layout="bnhd")
+
+    def layer(q, k, v):
+        o = gfa.flash_attn_gqa_op(q * 1.0, k, v, causal=True, slide_size=48, scale=0.05)
+        return o.transpose(1, 2).contiguous()
+
+    compiled = torch.compile(layer, backend="aot_eager", fullgraph=True)
+    res = []
+    for fn in (layer, compiled):
+        qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        o = fn(qq, kk, vv)
+        o.backward(do.transpose(1, 2))
+        res.append((o.detach(), qq.grad, kk.grad, vv.grad))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
