@@ -62,6 +62,11 @@ SMALL = [
     (1, 6, 3, 31, 256, True, 0, torch.bfloat16),    # odd group size
     (2, 8, 2, 160, 512, True, 0, torch.float16),    # batch > 1 at D=512
     (1, 8, 1, 130, 512, True, 40, torch.bfloat16),  # sliding window at D=512
+    (1, 6, 2, 100, 512, True, 0, torch.bfloat16),   # group size 3: one head per workgroup group
+    (1, 16, 1, 96, 256, True, 20, torch.float16),   # group size 16
+    (1, 4, 1, 257, 256, True, 100, torch.bfloat16), # window over many tiles, ragged N
+    (2, 8, 2, 65, 512, False, 0, torch.float16),    # non-causal, batch > 1, D=512
+    (1, 2, 1, 64, 512, True, 63, torch.bfloat16),   # window = N - 1
 ]
 
 
