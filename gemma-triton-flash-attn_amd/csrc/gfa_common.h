@@ -212,11 +212,7 @@ struct TileLoader {
 
   __device__ __forceinline__ void load(int row0, char GFA_LDS* tile) const {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int grp = i * NW + wave;
-      const unsigned soff = (unsigned)(row0 + grp * RPI) * stride_b;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void GFA_LDS*)(tile + grp * 1024), 16, voff[i % NV], soff, 0, 0);
-    }
+    for (int i = 0; i < NI; ++i) load_part(i, row0, tile);
   }
 };
 
