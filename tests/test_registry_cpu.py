@@ -1,0 +1,73 @@
+"""Row R5 (the HEAD_DIM-keyed registry) on the CPU.
+
+1. The oracle's restatement of the reference's Triton tile selection reproduces the
+   reference's own known-answer table (context/baseline.md:1582-1592) and its forward /
+   dQ defaults (attention.py:1444-1451, 1498-1504).
+2. The engine's registry, which replaces those tables with gfx950 tiles, gives fixed
+   known answers on the BASELINE shapes: a change of the rule shows up here.
+"""
+from __future__ import annotations
+
+import pytest
+
+import gemma_triton_flash_attn_amd as gfa
+from oracle import reference_registry as rr
+
+# context/baseline.md:1582-1592: (config, Hkv, N) -> (BKV, QS, grid), D=256 (the D<512
+# branch), B=1. Config A has H_KV=16, config B H_KV=1.
+KNOWN = [
+    (16, 1024, 64, 1, 256),
+    (16, 2048, 64, 1, 512),
+    (16, 4096, 64, 1, 1024),
+    (1, 1024, 64, 8, 128),    # "rescue": tiny grid takes the big tile and QS=8
+    (1, 2048, 32, 4, 256),
+    (1, 4096, 32, 2, 256),
+    (1, 8192, 64, 1, 128),
+]
+
+
+@pytest.mark.parametrize("Hkv,N,bkv,qs,grid", KNOWN)
+def test_reference_dkv_selection_known_answers(Hkv, N, bkv, qs, grid):
+    t = rr.dkv_tiles(1, Hkv, N, 256)
+    assert (t["BLOCK_KV"], t["Q_SPLITS"], t["grid"]) == (bkv, qs, grid)
+
+
+@pytest.mark.parametrize("Hkv,N", [(4, 1024), (4, 8192), (2, 32768), (1, 4096)])
+def test_reference_dkv_d512_row(Hkv, N):
+    """'D=512 any | 16 | 1': BKV = 16 and no Q split at the reference's D=512 shapes."""
+    t = rr.dkv_tiles(1, Hkv, N, 512)
+    assert (t["BLOCK_KV"], t["BLOCK_Q"], t["num_warps"], t["Q_SPLITS"]) == (16, 64, 4, 1)
+
+
+def test_reference_forward_and_dq_defaults():
+    assert rr.forward_tiles(16384, 512) == {"BLOCK_Q": 64, "BLOCK_KV": 32, "num_warps": 8, "num_stages": 2}
+    assert rr.forward_tiles(16384, 256) == {"BLOCK_Q": 128, "BLOCK_KV": 64, "num_warps": 8, "num_stages": 2}
+    assert rr.forward_tiles(40, 256)["BLOCK_Q"] == 64 and rr.forward_tiles(40, 256)["BLOCK_KV"] == 64
+    assert rr.dq_tiles(16384, 512) == {"BLOCK_Q": 32, "BLOCK_KV": 64, "num_warps": 8}
+    assert rr.dq_tiles(16384, 256) == {"BLOCK_Q": 64, "BLOCK_KV": 64, "num_warps": 4}
+
+
+# The engine's registry on the BASELINE shapes (B, Hq, Hkv, N, D) -> chosen tiles.
+ENGINE_KNOWN = {
+    (1, 32, 4, 16384, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
+                                 q_splits=1),
+    (1, 32, 4, 8192, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
+                                q_splits=1),
+    (1, 16, 2, 32768, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
+                                 q_splits=1),
+    (1, 16, 8, 16384, 256): dict(fwd_block_q=64, fwd_block_kv=32, dq_block_q=64, dkv_block_kv=128, dkv_block_q=32,
+                                 q_splits=1),
+    (1, 32, 4, 1024, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
+                                q_splits=4),
+    # group size 8 packs 4 heads x 1 query block per forward / dQ workgroup; the 16-workgroup
+    # key grid needs the largest query split
+    (1, 8, 1, 2048, 256): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=128, dkv_block_q=32,
+                               q_splits=8),
+}
+
+
+@pytest.mark.parametrize("shape", list(ENGINE_KNOWN))
+def test_engine_registry_known_answers(shape):
+    cfg = gfa.get_config(*shape)
+    for key, want in ENGINE_KNOWN[shape].items():
+        assert cfg[key] == want, (key, cfg[key], want)
