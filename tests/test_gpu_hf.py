@@ -26,7 +26,7 @@ from oracle import attention_oracle as orc  # noqa: E402
 
 
 def _cos_rel(a, b):
-    a, b = a.float().flatten(), b.float().flatten()
+    a, b = a.detach().float().flatten(), b.detach().float().flatten()
     cos = float(torch.nn.functional.cosine_similarity(a, b, dim=0))
     rel = float(torch.linalg.vector_norm(a - b) / torch.linalg.vector_norm(b))
     return cos, rel
