@@ -28,9 +28,21 @@ from .registry import lookup
 _DTYPES = {torch.float16: _lib.GFA_DTYPE_FP16, torch.bfloat16: _lib.GFA_DTYPE_BF16}
 
 
-def _needs_copy(t: torch.Tensor) -> bool:
+# One (batch, head) slice must span at most 4 GiB: the kernels address tiles through 32-bit
+# buffer offsets (gfa_api.hip, check_span).
+_SLICE_LIMIT = 0xFFFFFFFF
+
+
+def _layout_ok(t: torch.Tensor) -> bool:
+    """Strides the ABI can use: unit head-dim stride, other strides non-negative multiples
+    of 8 elements, and one (batch, head) slice within the 4 GiB buffer range."""
     s = t.stride()
-    return (s[3] != 1 or any(x % 8 for x in s[:3]) or any(x < 0 for x in s[:3]) or t.data_ptr() % 16 != 0)
+    return (s[3] == 1 and all(x % 8 == 0 and x >= 0 for x in s[:3])
+            and ((t.shape[2] - 1) * s[2] + t.shape[3]) * t.element_size() <= _SLICE_LIMIT)
+
+
+def _needs_copy(t: torch.Tensor) -> bool:
+    return not _layout_ok(t) or t.data_ptr() % 16 != 0
 
 
 def _prep(t: torch.Tensor) -> torch.Tensor:

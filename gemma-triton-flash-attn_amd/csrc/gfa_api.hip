@@ -101,6 +101,19 @@ int check_view(const char* name, const void* ptr, const gfa_strides& s, bool nee
   return GFA_OK;
 }
 
+// The kernels move tiles with buffer instructions whose record count and offsets are 32-bit,
+// one buffer resource per (batch, head) slice, so one slice (N rows at the row stride) must
+// fit in 4 GiB. Contiguous (B, H, N, D) tensors reach that only at N * D > 2^31.
+int check_span(const char* name, const gfa_strides& s, int N, int D) {
+  const long long span = ((long long)(N - 1) * s.row + D) * 2;
+  if (span > 0xFFFFFFFFll)
+    return fail(GFA_ERR_UNSUPPORTED,
+                "%s: one (batch, head) slice spans %lld bytes; the tile copies address at most 4 GiB per slice "
+                "(a contiguous (B, H, N, D) layout spans N * D * 2 bytes)",
+                name, span);
+  return GFA_OK;
+}
+
 int check_dims(int B, int Hq, int Hkv, int N, int D, int dtype, int window) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || N <= 0)
     return fail(GFA_ERR_INVALID_ARGUMENT, "empty problem: B=%d Hq=%d Hkv=%d N=%d", B, Hq, Hkv, N);
@@ -150,6 +163,12 @@ int gfa_fwd(const gfa_fwd_args* a) {
   if ((rc = check_view("k", a->k, a->k_strides, true))) return rc;
   if ((rc = check_view("v", a->v, a->v_strides, true))) return rc;
   if ((rc = check_view("o", a->o, a->o_strides, true))) return rc;
+  {
+    const char* names[] = {"q", "k", "v", "o"};
+    const gfa_strides* views[] = {&a->q_strides, &a->k_strides, &a->v_strides, &a->o_strides};
+    for (int i = 0; i < 4; ++i)
+      if ((rc = check_span(names[i], *views[i], a->seq_len, a->head_dim))) return rc;
+  }
   if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
   const Entry* e = lookup(a->head_dim);
   const int bkv = a->block_kv ? a->block_kv : e->fwd_bkv;
@@ -213,6 +232,13 @@ int gfa_bwd(const gfa_bwd_args* a) {
   if ((rc = check_view("dq", a->dq, a->dq_strides, true))) return rc;
   if ((rc = check_view("dk", a->dk, a->dk_strides, true))) return rc;
   if ((rc = check_view("dv", a->dv, a->dv_strides, true))) return rc;
+  {
+    const char* names[] = {"q", "k", "v", "o", "dout", "dq", "dk", "dv"};
+    const gfa_strides* views[] = {&a->q_strides, &a->k_strides, &a->v_strides, &a->o_strides,
+                                  &a->do_strides, &a->dq_strides, &a->dk_strides, &a->dv_strides};
+    for (int i = 0; i < 8; ++i)
+      if ((rc = check_span(names[i], *views[i], a->seq_len, a->head_dim))) return rc;
+  }
   if (a->lse == nullptr || a->delta == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "lse and delta are required");
   if (a->lse_ld < GFA_LSE_LD(a->seq_len) || (a->lse_ld & 3) || !aligned16(a->lse) || !aligned16(a->delta))
     return fail(GFA_ERR_INVALID_ARGUMENT, "lse_ld=%d must be >= %d (multiple of 4, 16-byte aligned lse/delta)",

@@ -17,16 +17,15 @@ from __future__ import annotations
 
 import torch
 
-from .attention import _backward, _check_inputs, _default_scale, _forward, _norm_window, _prep, lse_ld
+from .attention import _backward, _check_inputs, _default_scale, _forward, _layout_ok, _norm_window, _prep, lse_ld
 
 
 def _out_like(t: torch.Tensor) -> torch.Tensor:
-    """Output buffer with t's layout, or contiguous when that layout breaks the ABI's row
-    rules (the same choice the eager path makes; fake tensors have no data pointer, and real
-    allocations are always 16-byte aligned, so only the strides are checked)."""
+    """Output buffer with t's layout, or contiguous when that layout breaks the ABI's rules
+    (the same choice the eager path makes; fake tensors have no data pointer, and real
+    allocations are always 16-byte aligned, so only the layout is checked)."""
     o = torch.empty_like(t)
-    s = o.stride()
-    if s[3] != 1 or any(x % 8 for x in s[:3]):
+    if not _layout_ok(o):
         o = torch.empty(t.shape, dtype=t.dtype, device=t.device)
     return o
 

@@ -160,3 +160,23 @@ def test_register_into_transformers():
     assert "triton_gqa" in AttentionInterface._global_mapping
     gfa.register_triton_attention("gfa_custom")
     assert ALL_ATTENTION_FUNCTIONS.get_interface("gfa_custom", None) is gfa.triton_gqa_attention
+
+
+def test_slice_span_over_4gib_is_rejected():
+    """One (batch, head) slice at the row stride must fit the kernels' 32-bit buffer range:
+    HF's (B, N, H, D) layout with 32 heads of 512 at N = 2^17 + 1 spans just over 4 GiB."""
+    lib = _lib.load()
+    n, row = 131073, 32 * 512
+    a = _fwd_args(seq_len=n, lse_ld=(n + 63) // 64 * 64, q_strides=_lib.Strides(n * row, 512, row))
+    assert lib.gfa_fwd(ctypes.byref(a)) == 2
+    assert b"4 GiB" in lib.gfa_last_error()
+    # the Python layer copies such a view to the contiguous layout, which fits
+    import torch
+
+    from gemma_triton_flash_attn_amd.attention import _layout_ok
+
+    def view(strides):
+        return torch.empty_strided((1, 32, n, 512), strides, dtype=torch.bfloat16, device="meta")
+
+    assert not _layout_ok(view((n * row, 512, row, 1)))
+    assert _layout_ok(view((32 * n * 512, n * 512, 512, 1)))
