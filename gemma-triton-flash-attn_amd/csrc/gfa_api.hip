@@ -121,6 +121,12 @@ int check_dims(int B, int Hq, int Hkv, int N, int D, int dtype, int window) {
   if (lookup(D) == nullptr) return fail(GFA_ERR_UNSUPPORTED, "head_dim=%d is not in the registry (256, 512)", D);
   if (dtype != GFA_DTYPE_FP16 && dtype != GFA_DTYPE_BF16) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
   if (window < 0) return fail(GFA_ERR_INVALID_ARGUMENT, "window=%d must be >= 0", window);
+  // Every grid is at most one workgroup per 32-row block of every query head (forward, dQ)
+  // or per 32 keys of every KV head and query split (dK/dV, up to 8 splits); grid sizes are
+  // 32-bit.
+  const long long blocks = ((long long)N + 31) / 32;
+  if (blocks * B * Hq > 0x7fffffffll || blocks * B * Hkv * 8 > 0x7fffffffll)
+    return fail(GFA_ERR_UNSUPPORTED, "B=%d Hq=%d N=%d needs more workgroups than one launch grid holds", B, Hq, N);
   return GFA_OK;
 }
 

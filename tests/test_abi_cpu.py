@@ -180,3 +180,12 @@ def test_slice_span_over_4gib_is_rejected():
 
     assert not _layout_ok(view((n * row, 512, row, 1)))
     assert _layout_ok(view((32 * n * 512, n * 512, 512, 1)))
+
+
+def test_grid_larger_than_one_launch_is_rejected():
+    lib = _lib.load()
+    a = _fwd_args(batch=1100000, heads_q=1024, heads_kv=1024)  # 2 x 1.1e6 x 1024 > 2^31 workgroups
+    for s in ("q_strides", "k_strides", "v_strides", "o_strides"):
+        setattr(a, s, _lib.Strides(1024 * 64 * 512, 64 * 512, 512))
+    assert lib.gfa_fwd(ctypes.byref(a)) == 2
+    assert b"launch grid" in lib.gfa_last_error()
