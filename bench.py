@@ -43,6 +43,9 @@ WORKLOADS = {
     "d256_swa1024_gqa2_n16k": dict(B=1, Hq=16, Hkv=8, N=16384, D=256, causal=True, window=1024, dtype="bf16", amp=1.0),
     "c2_d512_causal_gqa8_n8k": dict(B=1, Hq=32, Hkv=4, N=8192, D=512, causal=True, window=0, dtype="bf16", amp=1.0),
     "c4_d512_causal_gqa8_n32k": dict(B=1, Hq=16, Hkv=2, N=32768, D=512, causal=True, window=0, dtype="fp16", amp=0.5),
+    # the rest of the reference's documented head-dim range (64-512): not Gemma-4 layers
+    "d128_causal_gqa4_n16k": dict(B=1, Hq=32, Hkv=8, N=16384, D=128, causal=True, window=0, dtype="bf16", amp=1.0),
+    "d64_causal_mha_n16k": dict(B=1, Hq=32, Hkv=32, N=16384, D=64, causal=True, window=0, dtype="bf16", amp=1.0),
 }
 
 
@@ -343,7 +346,8 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--all", action="store_true", help="also time BASELINE configs 2 and 4")
+    ap.add_argument("--all", action="store_true",
+                    help="also time BASELINE configs 2 and 4 and the D=128 / D=64 workloads")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernels", action="store_true", help="skip per-kernel timing")
     ap.add_argument("--workloads", default="d512_causal_gqa8_n16k,d256_swa1024_gqa2_n16k",
@@ -387,8 +391,10 @@ def main(argv=None):
         print(json.dumps({"metric": METRIC, "workloads": results}), flush=True)
         return 0
     if args.all:
-        for name in ("c2_d512_causal_gqa8_n8k", "c4_d512_causal_gqa8_n32k"):
-            results[name] = bench_workload(name, WORKLOADS[name], args.steps, args.warmup, device, kernels=False)
+        for name in ("c2_d512_causal_gqa8_n8k", "c4_d512_causal_gqa8_n32k", "d128_causal_gqa4_n16k",
+                     "d64_causal_mha_n16k"):
+            results[name] = bench_workload(name, WORKLOADS[name], args.steps, args.warmup, device,
+                                           kernels=name.startswith(("d128", "d64")) and not args.no_kernels)
 
     e2e = None
     if not args.no_e2e:

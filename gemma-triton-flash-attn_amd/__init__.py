@@ -14,7 +14,7 @@ computed by hand-written HIP kernels behind a C ABI (include/gfa.h, libgfa.so):
     register_triton_attention(name="triton_gqa"), triton_gqa_attention   HF integration
     REGISTRY / get_config                                                HEAD_DIM-keyed configs
 
-q: (B, N_Q_HEADS, N, D), k/v: (B, N_KV_HEADS, N, D), fp16/bf16, D in {256, 512}.
+q: (B, N_Q_HEADS, N, D), k/v: (B, N_KV_HEADS, N, D), fp16/bf16, D in {64, 128, 256, 512}.
 """
 from .attention import FlashAttnGQAFunction, attention, attention_flash_gqa, flash_attn_gqa_train
 from .ops import flash_attn_gqa_op

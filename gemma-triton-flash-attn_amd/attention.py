@@ -198,7 +198,7 @@ class FlashAttnGQAFunction(torch.autograd.Function):
 def flash_attn_gqa_train(q, k, v, causal=False, slide_size=0, *, scale=None):
     """Flash attention with autograd support (reference attention.py:1625-1635).
 
-    q: (B, N_Q_HEADS, N, D); k, v: (B, N_KV_HEADS, N, D); fp16 or bf16; D in {256, 512}.
+    q: (B, N_Q_HEADS, N, D); k, v: (B, N_KV_HEADS, N, D); fp16 or bf16; D in {64, 128, 256, 512}.
     ``scale`` defaults to 1/sqrt(D) like the reference; other values are used natively.
     """
     return FlashAttnGQAFunction.apply(q, k, v, causal, slide_size, scale)

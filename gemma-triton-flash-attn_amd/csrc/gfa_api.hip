@@ -47,6 +47,8 @@ struct Entry {
 constexpr Entry kRegistry[] = {
     {512, 32, 4, 32, 4, 2, 32, 4, 2},
     {256, 32, 4, 32, 4, 1, 32, 4, 1},
+    {128, 64, 4, 32, 4, 1, 32, 4, 1},
+    {64, 64, 4, 32, 4, 1, 32, 4, 1},
 };
 
 const Entry* lookup(int d) {
@@ -56,7 +58,7 @@ const Entry* lookup(int d) {
 }
 
 bool fwd_built(int d, int bkv, int nw) {
-  return nw == 4 && ((d == 512 && bkv == 32) || (d == 256 && (bkv == 32 || bkv == 64)));
+  return nw == 4 && ((d == 512 && bkv == 32) || (d <= 256 && (bkv == 32 || bkv == 64)));
 }
 
 int largest_pow2_divisor_le(int r, int cap) {
@@ -118,7 +120,7 @@ int check_dims(int B, int Hq, int Hkv, int N, int D, int dtype, int window) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || N <= 0)
     return fail(GFA_ERR_INVALID_ARGUMENT, "empty problem: B=%d Hq=%d Hkv=%d N=%d", B, Hq, Hkv, N);
   if (Hq % Hkv != 0) return fail(GFA_ERR_INVALID_ARGUMENT, "heads_q=%d is not a multiple of heads_kv=%d", Hq, Hkv);
-  if (lookup(D) == nullptr) return fail(GFA_ERR_UNSUPPORTED, "head_dim=%d is not in the registry (256, 512)", D);
+  if (lookup(D) == nullptr) return fail(GFA_ERR_UNSUPPORTED, "head_dim=%d is not in the registry (64, 128, 256, 512)", D);
   if (dtype != GFA_DTYPE_FP16 && dtype != GFA_DTYPE_BF16) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
   if (window < 0) return fail(GFA_ERR_INVALID_ARGUMENT, "window=%d must be >= 0", window);
   // Every grid is at most one workgroup per 32-row block of every query head (forward, dQ)
@@ -142,7 +144,7 @@ int gfa_config(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len
                gfa_config_info* out) {
   if (out == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "out is NULL");
   const Entry* e = lookup(head_dim);
-  if (e == nullptr) return fail(GFA_ERR_UNSUPPORTED, "head_dim=%d is not in the registry (256, 512)", head_dim);
+  if (e == nullptr) return fail(GFA_ERR_UNSUPPORTED, "head_dim=%d is not in the registry (64, 128, 256, 512)", head_dim);
   if (heads_kv <= 0 || heads_q % heads_kv != 0 || batch <= 0 || seq_len <= 0)
     return fail(GFA_ERR_INVALID_ARGUMENT, "bad problem size");
   const gfa::QGrid g = make_qgrid(batch, heads_kv, heads_q / heads_kv, seq_len, e->fwd_waves);
@@ -330,7 +332,7 @@ int gfa_bwd(const gfa_bwd_args* a) {
   const int keys_per_wg = 32 * (e->dkv_waves / e->dkv_roles);
   pk.n_kb = (pk.N + keys_per_wg - 1) / keys_per_wg;
   pk.nblocks = pk.n_kb * pk.B * pk.Hkv * qs;
-  err = gfa::launch_bwd_dkv(pk, a->head_dim, e->dkv_bq, e->dkv_roles, bf16, stream);
+  err = gfa::launch_bwd_dkv(pk, a->head_dim, e->dkv_bq, e->dkv_waves, e->dkv_roles, bf16, stream);
   if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV launch failed: %s", hipGetErrorString(err));
   if (qs > 1) {
     err = gfa::launch_dkv_reduce(pk, a->head_dim, bf16, stream);

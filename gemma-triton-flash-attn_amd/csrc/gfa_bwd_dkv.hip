@@ -32,9 +32,10 @@ namespace gfa {
 
 // ROLES = 2: a wave pair per 32 keys, split by role (see above). ROLES = 1: one wave per
 // 32 keys does all four products (K and V rows resident, dV^T and dK^T both in AGPRs);
-// used where the head dim leaves room for both accumulators (D=256).
-template <int D, int BQ, bool IS_BF16, int NW, int ROLES>
-__global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams p) {
+// used where the head dim leaves room for both accumulators (D <= 256). WPE: waves per SIMD
+// the register budget is bounded for (D=64 fits two).
+template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE>
+__global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParams p) {
   constexpr int KT = D / 16;   // MFMA k-steps of the score products (full head dim)
   constexpr int DB = D / 32;   // 32-row blocks of the dV^T / dK^T accumulator
   constexpr int SB = BQ / 32;  // 32-query score blocks per tile
@@ -44,7 +45,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
   constexpr int NS = 3 - ROLES;                      // stationary operands / accumulators per wave
   static_assert(ROLES == 1 || ROLES == 2, "one wave or a role-split pair per 32 keys");
   static_assert(BQ % 32 == 0, "BQ must be a multiple of 32");
-  static_assert(D % 128 == 0, "head dim must be 256 or 512");
+  static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
 
   __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NU * PX];
   char GFA_LDS* smem = (char GFA_LDS*)smem_raw;
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
 
   int roff[8];  // tile rows (A operand of S / dP): row l32, chunk 2*kk + h  (+256 * (kk >> 3))
 #pragma unroll
-  for (int kl = 0; kl < 8; ++kl) roff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz(l32)) << 4);
+  for (int kl = 0; kl < 8; ++kl) roff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4);
   int toffA[4], toffB[4];  // tiles read transposed (A operands of dV^T, dK^T)
   {
     const int t16 = lane & 15;
@@ -130,8 +131,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dkv_kernel(const BwdDkvParams 
 #pragma unroll
     for (int dl = 0; dl < 4; ++dl) {
       const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
-      toffA[dl] = rA * (2 * D) + ((c ^ swz(rA)) << 4) + (t16 & 1) * 8;
-      toffB[dl] = rB * (2 * D) + ((c ^ swz(rB)) << 4) + (t16 & 1) * 8;
+      toffA[dl] = rA * (2 * D) + ((c ^ swz<D>(rA)) << 4) + (t16 & 1) * 8;
+      toffB[dl] = rB * (2 * D) + ((c ^ swz<D>(rB)) << 4) + (t16 & 1) * 8;
     }
   }
 
@@ -410,27 +411,35 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const BwdDkvParams p, i
 }
 
 // Explicit instantiations of every built variant (device code and host launch stubs).
-template __global__ void bwd_dkv_kernel<512, 32, true, 4, 2>(const BwdDkvParams);
-template __global__ void bwd_dkv_kernel<512, 32, false, 4, 2>(const BwdDkvParams);
-template __global__ void bwd_dkv_kernel<256, 32, true, 4, 1>(const BwdDkvParams);
-template __global__ void bwd_dkv_kernel<256, 32, false, 4, 1>(const BwdDkvParams);
+#define GFA_DKV_INST(DD, BB, WW, RR, EE)                                              \
+  template __global__ void bwd_dkv_kernel<DD, BB, true, WW, RR, EE>(const BwdDkvParams);  \
+  template __global__ void bwd_dkv_kernel<DD, BB, false, WW, RR, EE>(const BwdDkvParams);
+GFA_DKV_INST(512, 32, 4, 2, 1)
+GFA_DKV_INST(256, 32, 4, 1, 1)
+GFA_DKV_INST(128, 32, 4, 1, 1)
+GFA_DKV_INST(64, 32, 4, 1, 2)
+#undef GFA_DKV_INST
 template __global__ void dkv_reduce_kernel<true>(const BwdDkvParams, int);
 template __global__ void dkv_reduce_kernel<false>(const BwdDkvParams, int);
 
-template <int D, int BQ, bool IS_BF16, int NW, int ROLES>
+template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE>
 static hipError_t launch_dkv_t(const BwdDkvParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW, ROLES>), dim3(p.nblocks), dim3(NW * 64), 0, stream, p);
+  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW, ROLES, WPE>), dim3(p.nblocks), dim3(NW * 64), 0, stream, p);
   return hipGetLastError();
 }
 
-// Built dK/dV variants: (head dim, queries per tile, waves per 32 keys).
-hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, int roles, bool bf16, hipStream_t stream) {
-#define GFA_DKV_CASE(DD, BB, RR)                                                                   \
-  if (D == DD && bq == BB && roles == RR) {                                                        \
-    return bf16 ? launch_dkv_t<DD, BB, true, 4, RR>(p, stream) : launch_dkv_t<DD, BB, false, 4, RR>(p, stream); \
+// Built dK/dV variants: (head dim, queries per tile, waves per workgroup, waves per 32 keys,
+// waves per SIMD).
+hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, int nw, int roles, bool bf16, hipStream_t stream) {
+#define GFA_DKV_CASE(DD, BB, WW, RR, EE)                                                   \
+  if (D == DD && bq == BB && nw == WW && roles == RR) {                                    \
+    return bf16 ? launch_dkv_t<DD, BB, true, WW, RR, EE>(p, stream)                        \
+                : launch_dkv_t<DD, BB, false, WW, RR, EE>(p, stream);                      \
   }
-  GFA_DKV_CASE(512, 32, 2)
-  GFA_DKV_CASE(256, 32, 1)
+  GFA_DKV_CASE(512, 32, 4, 2, 1)
+  GFA_DKV_CASE(256, 32, 4, 1, 1)
+  GFA_DKV_CASE(128, 32, 4, 1, 1)
+  GFA_DKV_CASE(64, 32, 4, 1, 2)
 #undef GFA_DKV_CASE
   return hipErrorInvalidValue;
 }

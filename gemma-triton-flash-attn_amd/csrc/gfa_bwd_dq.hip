@@ -32,7 +32,9 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   constexpr int XCH = SPLIT == 2 ? 2 * XHALF : 0;     // S^T and dP^T partials of a pair
   static_assert(BKV % 32 == 0, "BKV must be a multiple of 32");
   static_assert(SPLIT == 1 || SPLIT == 2, "one wave or a wave pair per 32 query rows");
-  static_assert(DH % 128 == 0, "head dim must be 256 or 512");
+  static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
+  // The swizzle permutes 16-chunk groups, so a head-dim half must be whole groups.
+  static_assert(SPLIT == 1 || DH % 128 == 0, "a head-dim split needs halves of 128 or more elements");
 
   // Four distinct LDS tile objects (not one array indexed by a buffer id): with the loop
   // unrolled by two every access names its buffer statically, so the compiler's wait
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 
   int koff[8];
 #pragma unroll
-  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz(l32)) << 4) + dh * DH * 2;
+  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4) + dh * DH * 2;
   int toffA[4], toffB[4];  // K tile read transposed (A operand of dQ^T = K^T dS^T)
   {
     const int t16 = lane & 15;
@@ -140,8 +142,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 #pragma unroll
     for (int dl = 0; dl < 4; ++dl) {
       const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
-      toffA[dl] = rA * (2 * D) + ((c ^ swz(rA)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
-      toffB[dl] = rB * (2 * D) + ((c ^ swz(rB)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
+      toffA[dl] = rA * (2 * D) + ((c ^ swz<D>(rA)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
+      toffB[dl] = rB * (2 * D) + ((c ^ swz<D>(rB)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
     }
   }
   char GFA_LDS* xmine = xch + wave * XCH + lane * 16;
@@ -267,6 +269,10 @@ template __global__ void bwd_dq_kernel<512, 32, true, 4, 2>(const BwdDqParams);
 template __global__ void bwd_dq_kernel<512, 32, false, 4, 2>(const BwdDqParams);
 template __global__ void bwd_dq_kernel<256, 32, true, 4, 1>(const BwdDqParams);
 template __global__ void bwd_dq_kernel<256, 32, false, 4, 1>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<128, 32, true, 4, 1>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<128, 32, false, 4, 1>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<64, 32, true, 4, 1>(const BwdDqParams);
+template __global__ void bwd_dq_kernel<64, 32, false, 4, 1>(const BwdDqParams);
 
 template <int D, int BKV, bool IS_BF16, int NW, int SPLIT>
 static hipError_t launch_dq_t(const BwdDqParams& p, hipStream_t stream) {
@@ -274,12 +280,16 @@ static hipError_t launch_dq_t(const BwdDqParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Built dQ variants: D=512 on wave pairs (head-dim halves), D=256 one wave per 32 rows.
+// Built dQ variants: D=512 on wave pairs (head-dim halves), D=256/128/64 one wave per 32 rows.
 hipError_t launch_bwd_dq(const BwdDqParams& p, int D, int bkv, int split, bool bf16, hipStream_t stream) {
   if (D == 512 && bkv == 32 && split == 2)
     return bf16 ? launch_dq_t<512, 32, true, 4, 2>(p, stream) : launch_dq_t<512, 32, false, 4, 2>(p, stream);
   if (D == 256 && bkv == 32 && split == 1)
     return bf16 ? launch_dq_t<256, 32, true, 4, 1>(p, stream) : launch_dq_t<256, 32, false, 4, 1>(p, stream);
+  if (D == 128 && bkv == 32 && split == 1)
+    return bf16 ? launch_dq_t<128, 32, true, 4, 1>(p, stream) : launch_dq_t<128, 32, false, 4, 1>(p, stream);
+  if (D == 64 && bkv == 32 && split == 1)
+    return bf16 ? launch_dq_t<64, 32, true, 4, 1>(p, stream) : launch_dq_t<64, 32, false, 4, 1>(p, stream);
   return hipErrorInvalidValue;
 }
 

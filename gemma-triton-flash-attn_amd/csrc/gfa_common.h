@@ -111,20 +111,33 @@ __device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x))
 __device__ __forceinline__ void pin_vgpr(i16x8& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin_vgpr(f32x16& x) { asm volatile("" : "+v"(x)); }
 
-// XOR swizzle of the 16-byte chunk index inside one LDS tile row (only the low 4 bits
-// of the chunk index change). Two read patterns must be bank-conflict free (64 banks):
-//  * ds_read_b128, 16 lanes per cycle: one chunk column across 16 consecutive rows
-//    -> swz must be a bijection on row bits 0..3;
+// XOR swizzle of the 16-byte chunk index inside one LDS tile row. Two read patterns must be
+// bank-conflict free (64 banks of 4 bytes):
+//  * ds_read_b128, 16 lanes per cycle: one chunk column across 16 consecutive rows;
 //  * ds_read_b64_tr_b16, 32 lanes per cycle: 4 consecutive rows (aligned to 4) x an
-//    aligned group of 4 chunks -> swz bits 2..3 must be a bijection on row bits 0..1.
-// swz swaps the two bit pairs of the row index: chunk bits (2,3) <- row bits (0,1),
-// chunk bits (0,1) <- row bits (2,3).
-__device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
+//    aligned group of 4 chunks.
+// D >= 128 (16 or more chunks per row; only the low 4 bits of the chunk index change): the
+// first pattern needs swz to be a bijection on row bits 0..3, the second needs swz bits 2..3
+// to be a bijection on row bits 0..1. swz swaps the two bit pairs of the row index: chunk
+// bits (2,3) <- row bits (0,1), chunk bits (0,1) <- row bits (2,3).
+// D = 64 (8 chunks per row, so rows r and r+1 share one 256-byte bank line): the first
+// pattern needs swz to be a bijection from row bits 1..3 onto the 3-bit chunk index, the
+// second needs swz bit 2 to follow row bit 1. swz = chunk bit 2 <- row bit 1, chunk bits
+// (0,1) <- row bits (2,3).
+template <int D>
+__device__ __forceinline__ int swz(int row) {
+  static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
+  if constexpr (D >= 128) {
+    return ((row & 3) << 2) | ((row >> 2) & 3);
+  } else {
+    return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
+  }
+}
 
 // Byte offset of (row, 16B-chunk c) inside a tile whose rows hold D 16-bit elements.
 template <int D>
 __device__ __forceinline__ int tile_off(int row, int c) {
-  return row * (D * 2) + ((c ^ swz(row)) << 4);
+  return row * (D * 2) + ((c ^ swz<D>(row)) << 4);
 }
 
 __device__ __forceinline__ i16x8 lds_read16(const char GFA_LDS* base, int off) {
@@ -176,7 +189,7 @@ struct TileLoader {
   static constexpr int STEP_ROWS = NW * RPI;
   static constexpr int PERIOD = STEP_ROWS >= 16 ? 1 : 16 / STEP_ROWS;
   static constexpr int NV = NI < PERIOD ? NI : PERIOD;  // distinct lane offsets
-  static_assert(CPR >= 16 && CPR <= 64, "head dim must be 128..512");
+  static_assert(CPR >= 8 && CPR <= 64, "head dim must be 64..512");
   static_assert(BKV * CPR % (64 * NW) == 0, "tile must split evenly over the waves");
   static_assert(STEP_ROWS >= 16 ? STEP_ROWS % 16 == 0 : 16 % STEP_ROWS == 0, "swizzle period");
 
@@ -194,7 +207,7 @@ struct TileLoader {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int row = (i * NW + wave) * RPI + lrow;
-      voff[i] = lrow * stride_b + (unsigned)((lc ^ swz(row)) << 4);
+      voff[i] = lrow * stride_b + (unsigned)((lc ^ swz<D>(row)) << 4);
     }
   }
 

@@ -46,7 +46,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   // fp32 accumulators have range to spare.
   constexpr float kMargin = IS_BF16 ? 64.0f : 15.0f;
   static_assert(BKV % 32 == 0, "BKV must be a multiple of 32");
-  static_assert(D % 128 == 0, "head dim must be 128, 256 or 512");
+  static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
 
   // Four distinct LDS objects (not one array indexed by a buffer id): with the loop
   // unrolled by two every access names its buffer statically, so the compiler's wait
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   // the 16-byte chunk index, so chunk groups of 16 differ by a constant 256 bytes.
   int koff[8];  // K row l32, chunk 2*kk + h  (+256 * (kk >> 3))
 #pragma unroll
-  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz(l32)) << 4);
+  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4);
   int voffA[4], voffB[4];  // V read transposed: rows 4h + t/4 (+8), columns 32*db + ...
   {
     const int t16 = lane & 15;
@@ -126,8 +126,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
 #pragma unroll
     for (int dl = 0; dl < 4; ++dl) {
       const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
-      voffA[dl] = rA * (2 * D) + ((c ^ swz(rA)) << 4) + (t16 & 1) * 8;
-      voffB[dl] = rB * (2 * D) + ((c ^ swz(rB)) << 4) + (t16 & 1) * 8;
+      voffA[dl] = rA * (2 * D) + ((c ^ swz<D>(rA)) << 4) + (t16 & 1) * 8;
+      voffB[dl] = rB * (2 * D) + ((c ^ swz<D>(rB)) << 4) + (t16 & 1) * 8;
     }
   }
 
@@ -269,6 +269,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
 GFA_FWD_INST(512, 32, 4, 1)
 GFA_FWD_INST(256, 64, 4, 1)
 GFA_FWD_INST(256, 32, 4, 1)
+GFA_FWD_INST(128, 64, 4, 2)
+GFA_FWD_INST(128, 32, 4, 2)
+GFA_FWD_INST(64, 64, 4, 3)
+GFA_FWD_INST(64, 32, 4, 3)
 #undef GFA_FWD_INST
 
 template <int D, int BKV, bool IS_BF16, int NW, int WPE>
@@ -287,6 +291,10 @@ hipError_t launch_fwd(const FwdParams& p, int D, int bkv, int nw, bool bf16, hip
   GFA_FWD_CASE(512, 32, 4, 1)
   GFA_FWD_CASE(256, 64, 4, 1)
   GFA_FWD_CASE(256, 32, 4, 1)
+  GFA_FWD_CASE(128, 64, 4, 2)
+  GFA_FWD_CASE(128, 32, 4, 2)
+  GFA_FWD_CASE(64, 64, 4, 3)
+  GFA_FWD_CASE(64, 32, 4, 3)
 #undef GFA_FWD_CASE
   return hipErrorInvalidValue;
 }

@@ -28,6 +28,9 @@ CASES = [
     ("d256_full_gqa4", 1, 4, 1, 37, 256, False, 0),
     ("d8_causal_gqa3", 2, 6, 2, 19, 8, True, 0),
     ("d8_swa4_mha", 1, 3, 3, 23, 8, True, 4),
+    ("d128_swa9_gqa4", 1, 8, 2, 45, 128, True, 9),
+    ("d64_causal_gqa2", 2, 4, 2, 50, 64, True, 0),
+    ("d64_full_mha", 1, 2, 2, 29, 64, False, 0),
 ]
 
 

@@ -59,7 +59,9 @@ int main(void) {{
 
 
 @pytest.mark.parametrize("shape", [(1, 32, 4, 16384, 512), (1, 16, 8, 16384, 256), (2, 6, 3, 33, 256),
-                                   (1, 4, 4, 1, 512), (1, 8, 1, 1024, 512), (3, 16, 2, 32768, 512)])
+                                   (1, 4, 4, 1, 512), (1, 8, 1, 1024, 512), (3, 16, 2, 32768, 512),
+                                   (1, 32, 8, 16384, 128), (2, 8, 1, 300, 128), (1, 32, 32, 4096, 64),
+                                   (4, 12, 12, 77, 64)])
 def test_config_matches_python_registry(shape):
     assert _lib.config(*shape) == gfa.get_config(*shape)
 
@@ -78,7 +80,9 @@ def _fwd_args(**over):
 
 
 @pytest.mark.parametrize("over,status", [
-    (dict(head_dim=128), 2),
+    (dict(head_dim=96), 2),               # not a power of two
+    (dict(head_dim=32), 2),               # below the reference's documented 64-512
+    (dict(head_dim=1024), 2),
     (dict(heads_q=6, heads_kv=4), 1),
     (dict(seq_len=0), 1),
     (dict(dtype=7), 1),
@@ -131,8 +135,9 @@ def test_python_api_validation_needs_no_gpu():
         gfa.flash_attn_gqa_train(q, k, k, causal=True)
     with pytest.raises(TypeError):
         gfa.attention_flash_gqa(q, k.float(), k, causal=True)
-    with pytest.raises(ValueError, match="head_dim"):
-        gfa.attention_flash_gqa(q[..., :128], k[..., :128], k[..., :128])
+    for d in (96, 32):
+        with pytest.raises(ValueError, match="head_dim"):
+            gfa.attention_flash_gqa(q[..., :d], k[..., :d], k[..., :d])
     with pytest.raises(ValueError, match="multiple"):
         gfa.attention_flash_gqa(q[:, :3], k, k)
     with pytest.raises(ValueError):

@@ -24,7 +24,7 @@ def _capture(fn, warmup_stream):
     return g, out
 
 
-@pytest.mark.parametrize("D,window,q_splits", [(512, 0, 0), (256, 40, 0), (256, 0, 4)])
+@pytest.mark.parametrize("D,window,q_splits", [(512, 0, 0), (256, 40, 0), (256, 0, 4), (128, 0, 2), (64, 17, 0)])
 def test_graph_replay_matches_eager(D, window, q_splits, device):
     import gemma_triton_flash_attn_amd as gfa
     from gemma_triton_flash_attn_amd.attention import _backward, _forward

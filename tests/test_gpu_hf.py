@@ -3,11 +3,12 @@
 error < 0.05).
 
 * adapter unit: ``triton_gqa_attention`` on transformers' (B, H, N, D) views of
-  (B, N, H, D) projections, for a sliding D=256 and a full D=512 layer;
+  (B, N, H, D) projections, for sliding and full layers at every supported head dim;
 * in-model: a random-init Gemma-4 text model (GQA 8:1, sliding D=256 and full D=512
   layers) in bf16. Every attention call of its forward, with the model's own q/k/v views,
   scaling and sliding window, must match the oracle through the adapter (forward and
-  backward), and the whole model must run on the engine after the one-call registration.
+  backward), and the whole model must run on the engine after the one-call registration;
+* in-model, Llama: the same per-call check on a random-init Llama with head dim 128 / 64.
 """
 from __future__ import annotations
 
@@ -32,7 +33,7 @@ def _cos_rel(a, b):
     return cos, rel
 
 
-@pytest.mark.parametrize("D,window,causal", [(256, 48, True), (512, 0, True), (256, 0, False)])
+@pytest.mark.parametrize("D,window,causal", [(256, 48, True), (512, 0, True), (256, 0, False), (128, 32, True), (64, 0, False)])
 def test_adapter_unit(D, window, causal, device):
     import gemma_triton_flash_attn_amd as gfa
 
@@ -91,6 +92,57 @@ def test_gemma4_model_layers(device):
         grel = [_cos_rel(a.grad, b.grad)[1] for a, b in ((qq, qr), (kk, kr), (vv, vr))]
         print(f"  layer {i} D={q.shape[-1]} window={kw.get('sliding_window')}: O cos {cos:.6f} rel {rel:.2e}; "
               f"dQ/dK/dV rel {grel[0]:.2e} {grel[1]:.2e} {grel[2]:.2e}", flush=True)
+        assert cos > 0.999 and rel < 0.05
+        assert max(grel) < 0.05
+
+    got = logits_with(model, "triton_gqa", ids)
+    cos, rel = _cos_rel(got, ref)
+    print(f"  whole-model logits cos {cos:.6f} rel {rel:.3e}", flush=True)
+    assert torch.isfinite(got).all()
+    assert cos > 0.98
+
+
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_llama_model_layers(head_dim, device):
+    """The adapter is not tied to Gemma-4: a random-init Llama (GQA 4:1) with head dim 128 or
+    64, the rest of the reference's documented head-dim range, gives the oracle's result at
+    every attention call (forward and backward) and runs end to end on the engine."""
+    import gemma_triton_flash_attn_amd as gfa
+    from transformers import AttentionInterface, LlamaConfig, LlamaForCausalLM
+
+    print(f"case tiny llama head_dim={head_dim} N=300", flush=True)
+    gfa.register_triton_attention()
+    captured = []
+    oracle_attn = make_oracle_attention()
+
+    def capturing(module, query, key, value, attention_mask, **kwargs):
+        captured.append((module, query.detach(), key.detach(), value.detach(), dict(kwargs)))
+        return oracle_attn(module, query, key, value, attention_mask, **kwargs)
+
+    AttentionInterface.register("gfa_capture_llama", capturing)
+    cfg = LlamaConfig(vocab_size=1024, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=head_dim, max_position_embeddings=4096)
+    torch.manual_seed(0)
+    with torch.device(device):
+        model = LlamaForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval()
+    ids = torch.randint(0, cfg.vocab_size, (1, 300), generator=torch.Generator().manual_seed(0)).to(device)
+    ref = logits_with(model, "gfa_capture_llama", ids)
+    assert [c[1].shape[-1] for c in captured] == [head_dim, head_dim]
+
+    g = torch.Generator().manual_seed(2)
+    for i, (module, q, k, v, kw) in enumerate(captured):
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+        out, _ = gfa.triton_gqa_attention(module, qq, kk, vv, None, **kw)
+        qr, kr, vr = (t.float().clone().requires_grad_(True) for t in (q, k, v))
+        o_ref, _ = orc.forward_chunked(qr, kr, vr, module.is_causal, kw.get("sliding_window") or 0, kw.get("scaling"))
+        cos, rel = _cos_rel(out, o_ref.transpose(1, 2))
+        dout = torch.randn(out.shape, generator=g).to(device=device, dtype=out.dtype)
+        out.backward(dout)
+        o_ref.transpose(1, 2).backward(dout.float())
+        grel = [_cos_rel(a.grad, b.grad)[1] for a, b in ((qq, qr), (kk, kr), (vv, vr))]
+        print(f"  layer {i}: O cos {cos:.6f} rel {rel:.2e}; dQ/dK/dV rel {grel[0]:.2e} {grel[1]:.2e} {grel[2]:.2e}",
+              flush=True)
         assert cos > 0.999 and rel < 0.05
         assert max(grel) < 0.05
 

@@ -11,7 +11,8 @@ from conftest import make_inputs
 
 pytestmark = pytest.mark.gpu
 
-CASES = [(1, 8, 1, 128, 512, True, 0), (1, 4, 2, 96, 256, True, 40), (1, 2, 2, 64, 256, False, 0)]
+CASES = [(1, 8, 1, 128, 512, True, 0), (1, 4, 2, 96, 256, True, 40), (1, 2, 2, 64, 256, False, 0),
+         (1, 8, 2, 80, 128, True, 24), (2, 4, 4, 50, 64, False, 0)]
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,N,D,causal,window", CASES)

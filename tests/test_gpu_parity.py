@@ -67,6 +67,14 @@ SMALL = [
     (1, 4, 1, 257, 256, True, 100, torch.bfloat16), # window over many tiles, ragged N
     (2, 8, 2, 65, 512, False, 0, torch.float16),    # non-causal, batch > 1, D=512
     (1, 2, 1, 64, 512, True, 63, torch.bfloat16),   # window = N - 1
+    # D=128 and D=64 (the rest of the reference's documented 64-512 range)
+    (1, 8, 2, 200, 128, True, 0, torch.bfloat16),
+    (2, 4, 1, 131, 128, True, 37, torch.float16),
+    (1, 4, 4, 97, 128, False, 0, torch.bfloat16),
+    (1, 8, 1, 300, 64, True, 0, torch.float16),
+    (2, 6, 2, 77, 64, True, 16, torch.bfloat16),
+    (1, 2, 2, 45, 64, False, 0, torch.float16),
+    (1, 4, 1, 1, 64, True, 0, torch.bfloat16),      # N = 1 at D=64
 ]
 
 
@@ -84,7 +92,7 @@ def test_fwd_bwd_vs_oracle(B, Hq, Hkv, N, D, causal, window, dtype, device):
     assert max(errs) <= GRAD_TOL
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,N,D,causal,window,dtype", SMALL[:6])
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,causal,window,dtype", SMALL[:6] + [c for c in SMALL if c[4] < 256][:3])
 def test_lse_and_inference_path(B, Hq, Hkv, N, D, causal, window, dtype, device):
     from gemma_triton_flash_attn_amd.attention import _forward
 
@@ -105,7 +113,9 @@ def test_lse_and_inference_path(B, Hq, Hkv, N, D, causal, window, dtype, device)
 def test_golden_vectors(path, device):
     z = np.load(path)
     B, Hq, Hkv, N, D, causal, window = (int(x) for x in z["meta"])
-    if D not in (256, 512):
+    from gemma_triton_flash_attn_amd import SUPPORTED_HEAD_DIMS
+
+    if D not in SUPPORTED_HEAD_DIMS:
         pytest.skip("head dim outside the kernel set (oracle-only vector)")
     print(f"golden {os.path.basename(path)}", flush=True)
     q, k, v, do = (torch.from_numpy(z[n].view(np.int16)).view(torch.bfloat16).to(device) for n in ("q", "k", "v", "do"))
@@ -190,13 +200,14 @@ def test_late_large_scores(dtype, jump, device):
             assert _rel(_np(got), ref) <= GRAD_TOL
 
 
+@pytest.mark.parametrize("D", [256, 128, 64])
 @pytest.mark.parametrize("block_kv", [32, 64])
-def test_block_kv_override_d256(block_kv, device):
-    """attention_flash_gqa's BLOCK_KV picks one of the built D=256 forward tiles; every
-    choice matches the oracle and they agree with each other closely."""
+def test_block_kv_override(block_kv, D, device):
+    """attention_flash_gqa's BLOCK_KV picks one of the built forward tiles of the head dim;
+    every choice matches the oracle and they agree with each other closely."""
     import gemma_triton_flash_attn_amd as gfa
 
-    q, k, v, _ = make_inputs(1, 4, 2, 150, 256, torch.bfloat16, device, seed=21)
+    q, k, v, _ = make_inputs(1, 4, 2, 150, D, torch.bfloat16, device, seed=21)
     o = gfa.attention_flash_gqa(q, k, v, causal=True, slide_size=50, BLOCK_KV=block_kv)
     o_def = gfa.attention_flash_gqa(q, k, v, causal=True, slide_size=50)
     o_ref, _ = orc.forward(_np(q), _np(k), _np(v), True, 50)

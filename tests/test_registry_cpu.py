@@ -45,6 +45,10 @@ def test_reference_forward_and_dq_defaults():
     assert rr.forward_tiles(40, 256)["BLOCK_Q"] == 64 and rr.forward_tiles(40, 256)["BLOCK_KV"] == 64
     assert rr.dq_tiles(16384, 512) == {"BLOCK_Q": 32, "BLOCK_KV": 64, "num_warps": 8}
     assert rr.dq_tiles(16384, 256) == {"BLOCK_Q": 64, "BLOCK_KV": 64, "num_warps": 4}
+    # below D=256 the reference forward drops to 4 warps (attention.py:1448)
+    assert rr.forward_tiles(4096, 128) == {"BLOCK_Q": 128, "BLOCK_KV": 64, "num_warps": 4, "num_stages": 2}
+    assert rr.forward_tiles(4096, 64)["num_warps"] == 4
+    assert rr.dq_tiles(4096, 128) == {"BLOCK_Q": 64, "BLOCK_KV": 64, "num_warps": 4}
 
 
 # The engine's registry on the BASELINE shapes (B, Hq, Hkv, N, D) -> chosen tiles.
@@ -63,6 +67,14 @@ ENGINE_KNOWN = {
     # key grid needs the largest query split
     (1, 8, 1, 2048, 256): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=128, dkv_block_q=32,
                                q_splits=8),
+    # D=128 / D=64 (the rest of the reference's documented head-dim range): 64-key forward
+    # tiles, one wave per 32 keys in dK/dV
+    (1, 32, 8, 16384, 128): dict(fwd_block_q=32, fwd_block_kv=64, dq_block_q=32, dkv_block_kv=128, dkv_block_q=32,
+                                 q_splits=1),
+    (1, 8, 1, 4096, 128): dict(fwd_block_q=32, fwd_block_kv=64, dq_block_q=32, dkv_block_kv=128, dkv_block_q=32,
+                               q_splits=8),
+    (1, 32, 32, 4096, 64): dict(fwd_block_q=128, fwd_block_kv=64, dq_block_q=128, dkv_block_kv=128, dkv_block_q=32,
+                                q_splits=1),
 }
 
 
