@@ -79,13 +79,14 @@ gfa::QGrid make_qgrid(int B, int Hkv, int R, int N, int nu) {
   return g;
 }
 
-// Smallest of {1, 2, 4, 8} giving at least one workgroup per CU (256 CUs on MI355X).
-// units = 32-key units per dK/dV workgroup.
+// Smallest of {1, 2, 4, 8} giving at least four dK/dV workgroups per CU (256 CUs on MI355X):
+// below that, splitting the query range beats the cost of the fp32 partials (measured from
+// 64 to 1024 key-grid workgroups at D = 64..512). units = 32-key units per workgroup.
 int pick_q_splits(int B, int Hkv, int N, int units) {
   const int keys_per_wg = 32 * units;
   const int grid = ((N + keys_per_wg - 1) / keys_per_wg) * B * Hkv;
   int qs = 1;
-  while (qs < 8 && grid * qs < 256) qs *= 2;
+  while (qs < 8 && grid * qs < 4 * 256) qs *= 2;
   return qs;
 }
 

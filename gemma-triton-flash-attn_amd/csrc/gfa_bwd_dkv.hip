@@ -147,10 +147,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   const float* stat_kv0 = (role == 0 ? p.lse : p.delta) + stat_off;
   const float* stat_kv1 = p.delta + stat_off;
 
-  // Iteration `it` covers head kvh*R + r of query tile qt, it = r * nqt + (qt - qt_lo);
+  // Iteration `it` covers head kvh*R + r of query tile qt, it = (qt_hi - 1 - qt) * R + r:
+  // query tiles from the last one down, the R heads of a tile back to back. Under causal
+  // masking every key block's range ends at the same last tile, so the workgroups that run
+  // together walk the same Q / dO tiles at the same time and share them in L2.
   // (r_c, qt_c) walk it incrementally.
-  int r_c = nqt > 0 ? it_lo / nqt : 0;
-  int qt_c = nqt > 0 ? qt_lo + it_lo % nqt : 0;
+  int r_c = it_lo % p.R;
+  int qt_c = qt_hi - 1 - it_lo / p.R;
   if (it_lo < it_hi) {
     qload.rebase(q_kv + (int64_t)r_c * p.qv.sh, p.qv.sn, p.N);
     dload.rebase(d_kv + (int64_t)r_c * p.dov.sh, p.dov.sn, p.N);
@@ -317,10 +320,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     }
     // Next tile; the last iteration re-fetches its own tile into the idle buffer (never
     // read) so the loop body stays branch-free.
-    int r_n = r_c, qt_n = qt_c + 1;
-    if (qt_n == qt_hi) {
-      qt_n = qt_lo;
-      ++r_n;
+    int r_n = r_c + 1, qt_n = qt_c;
+    if (r_n == p.R) {
+      r_n = 0;
+      --qt_n;
     }
     if (it + 1 >= it_hi) {
       r_n = r_c;

@@ -82,16 +82,18 @@ def query_grid(batch: int, heads_q: int, heads_kv: int, seq_len: int, units: int
 
 
 def q_splits_for(batch: int, heads_kv: int, seq_len: int, units: int) -> int:
-    """Smallest of {1, 2, 4, 8} giving at least one dKV workgroup per CU (``units`` = 32-key
+    """Smallest of {1, 2, 4, 8} giving at least four dKV workgroups per CU (``units`` = 32-key
     units per workgroup).
 
     Same intent as the reference's Q_SPLITS rule (attention.py:1576-1587): split each key
-    block's query range only when the raw grid cannot fill the GPU.
+    block's query range only when the raw grid is small. The threshold of four rounds of
+    workgroups is where splitting stopped paying on MI355X (key grids of 64 to 1024
+    workgroups, D = 64..512).
     """
     keys_per_wg = 32 * units
     grid = -(-seq_len // keys_per_wg) * batch * heads_kv
     qs = 1
-    while qs < 8 and grid * qs < NUM_CUS:
+    while qs < 8 and grid * qs < 4 * NUM_CUS:
         qs *= 2
     return qs
 

@@ -56,13 +56,13 @@ ENGINE_KNOWN = {
     (1, 32, 4, 16384, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
                                  q_splits=1),
     (1, 32, 4, 8192, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
-                                q_splits=1),
+                                q_splits=2),   # 512-workgroup key grid: under four per CU
     (1, 16, 2, 32768, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
                                  q_splits=1),
     (1, 16, 8, 16384, 256): dict(fwd_block_q=64, fwd_block_kv=32, dq_block_q=64, dkv_block_kv=128, dkv_block_q=32,
                                  q_splits=1),
     (1, 32, 4, 1024, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
-                                q_splits=4),
+                                q_splits=8),
     # group size 8 packs 4 heads x 1 query block per forward / dQ workgroup; the 16-workgroup
     # key grid needs the largest query split
     (1, 8, 1, 2048, 256): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=128, dkv_block_q=32,
