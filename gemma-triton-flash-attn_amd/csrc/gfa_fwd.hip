@@ -47,6 +47,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   constexpr float kMargin = IS_BF16 ? 64.0f : 15.0f;
   static_assert(BKV % 32 == 0, "BKV must be a multiple of 32");
   static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
+  // LDS read-ahead of the score chain: shallower when several waves share a SIMD's registers.
+  constexpr int PF = WPE == 1 ? 4 : 2;
 
   // Four distinct LDS objects (not one array indexed by a buffer id): with the loop
   // unrolled by two every access names its buffer statically, so the compiler's wait
@@ -155,7 +157,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     const int rn = min(t + 1, t_hi - 1) * BKV;
     const int k0 = t * BKV;
     f32x16 s[SB];
-    s[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, 2 * NI>(kt, koff, 0, qf, [&](int i) {
+    s[0] = mma_chain1_lds_ld<IS_BF16, KT, PF, 2 * NI>(kt, koff, 0, qf, [&](int i) {
       if (i < NI) {
         kload.load_part(i, rn, kn);
       } else {
@@ -206,9 +208,14 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     // scheduling region, so its VALU work can fill the MFMA shadow.
     mma_tr_accumulate<IS_BF16, D, DB, BKV / 16, 2, 1>(acc, vt, voffA, voffB, pb);
     __builtin_amdgcn_sched_barrier(0);
-    // Keep O^T in AGPRs across iterations (the VGPRs hold Q and the working set).
+    // One wave per SIMD (D >= 256): keep O^T in AGPRs across iterations (the VGPRs hold Q
+    // and the working set). With several waves per SIMD (D <= 128) everything fits the
+    // VGPRs; left unpinned, the MFMAs then write VGPRs directly and the softmax needs no
+    // AGPR reads (5-10% faster there).
+    if constexpr (WPE == 1) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
+      for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
+    }
   };
 
   // One pass over the workgroup's key tiles. Written once, expanded twice below: the
