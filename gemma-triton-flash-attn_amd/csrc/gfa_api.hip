@@ -47,7 +47,7 @@ struct Entry {
 constexpr Entry kRegistry[] = {
     {512, 32, 4, 32, 4, 2, 32, 4, 2},
     {256, 32, 4, 32, 4, 1, 32, 4, 1},
-    {128, 64, 4, 32, 4, 1, 32, 4, 1},
+    {128, 64, 4, 32, 4, 1, 32, 4, 2},
     {64, 64, 4, 32, 4, 1, 32, 4, 1},
 };
 

@@ -423,8 +423,8 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const BwdDkvParams p, i
   template __global__ void bwd_dkv_kernel<DD, BB, false, WW, RR, EE>(const BwdDkvParams);
 GFA_DKV_INST(512, 32, 4, 2, 1)
 GFA_DKV_INST(256, 32, 4, 1, 1)
-GFA_DKV_INST(128, 32, 4, 1, 1)
 GFA_DKV_INST(64, 32, 4, 1, 2)
+GFA_DKV_INST(128, 32, 4, 2, 2)
 #undef GFA_DKV_INST
 template __global__ void dkv_reduce_kernel<true>(const BwdDkvParams, int);
 template __global__ void dkv_reduce_kernel<false>(const BwdDkvParams, int);
@@ -445,8 +445,8 @@ hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, int nw, int role
   }
   GFA_DKV_CASE(512, 32, 4, 2, 1)
   GFA_DKV_CASE(256, 32, 4, 1, 1)
-  GFA_DKV_CASE(128, 32, 4, 1, 1)
   GFA_DKV_CASE(64, 32, 4, 1, 2)
+  GFA_DKV_CASE(128, 32, 4, 2, 2)
 #undef GFA_DKV_CASE
   return hipErrorInvalidValue;
 }

@@ -42,7 +42,7 @@ REGISTRY: dict[int, KernelConfig] = {
                       dkv_waves=4, dkv_roles=1,
                       fwd_block_kv_options=(32, 64)),
     128: KernelConfig(128, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
-                      dkv_waves=4, dkv_roles=1,
+                      dkv_waves=4, dkv_roles=2,
                       fwd_block_kv_options=(32, 64)),
     64: KernelConfig(64, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
                      dkv_waves=4, dkv_roles=1,

@@ -68,10 +68,11 @@ ENGINE_KNOWN = {
     (1, 8, 1, 2048, 256): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=128, dkv_block_q=32,
                                q_splits=8),
     # D=128 / D=64 (the rest of the reference's documented head-dim range): 64-key forward
-    # tiles, one wave per 32 keys in dK/dV
-    (1, 32, 8, 16384, 128): dict(fwd_block_q=32, fwd_block_kv=64, dq_block_q=32, dkv_block_kv=128, dkv_block_q=32,
+    # tiles; dK/dV on role-split pairs (64 keys per workgroup) at D=128, one wave per 32 keys
+    # at D=64
+    (1, 32, 8, 16384, 128): dict(fwd_block_q=32, fwd_block_kv=64, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
                                  q_splits=1),
-    (1, 8, 1, 4096, 128): dict(fwd_block_q=32, fwd_block_kv=64, dq_block_q=32, dkv_block_kv=128, dkv_block_q=32,
+    (1, 8, 1, 4096, 128): dict(fwd_block_q=32, fwd_block_kv=64, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
                                q_splits=8),
     (1, 32, 32, 4096, 64): dict(fwd_block_q=128, fwd_block_kv=64, dq_block_q=128, dkv_block_kv=128, dkv_block_q=32,
                                 q_splits=1),
