@@ -32,8 +32,9 @@ namespace gfa {
 
 // ROLES = 2: a wave pair per 32 keys, split by role (see above). ROLES = 1: one wave per
 // 32 keys does all four products (K and V rows resident, dV^T and dK^T both in AGPRs);
-// used where the head dim leaves room for both accumulators (D <= 256). WPE: waves per SIMD
-// the register budget is bounded for (D=64 fits two).
+// used at D=256 and D=64, where that is faster than the pair. Role-split pairs run D=512
+// (one wave per SIMD) and D=128 (two). WPE: waves per SIMD the register budget is bounded
+// for.
 template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE>
 __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParams p) {
   constexpr int KT = D / 16;   // MFMA k-steps of the score products (full head dim)

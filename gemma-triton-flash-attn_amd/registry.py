@@ -6,8 +6,8 @@ launch code (/root/reference/flash_attn/attention.py:561-579 inference forward,
 same role is one explicit table. Each entry names the tiles of the three gfx950 kernels:
 the forward runs one wave per 32 query rows over the full head dim, the dQ kernel
 ``dq_split`` waves per 32 query rows (a pair splitting the head dim at D=512, one wave at
-D <= 256), the dK/dV kernel ``dkv_roles`` waves per 32 keys (a role-split pair at D=512,
-one wave doing all four products at D <= 256). D=64 and D=128 cover the rest of the
+D <= 256), the dK/dV kernel ``dkv_roles`` waves per 32 keys (a role-split pair at D=512 and
+D=128, one wave doing all four products at D=256 and D=64). D=64 and D=128 cover the rest of the
 reference's documented head-dim range (64-512, powers of two; docs/api.md:63).
 
 The C library holds the same table (csrc/gfa_api.hip, kRegistry); ``gfa_config`` reports
