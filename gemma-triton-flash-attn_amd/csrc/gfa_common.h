@@ -134,12 +134,6 @@ __device__ __forceinline__ int swz(int row) {
   }
 }
 
-// Byte offset of (row, 16B-chunk c) inside a tile whose rows hold D 16-bit elements.
-template <int D>
-__device__ __forceinline__ int tile_off(int row, int c) {
-  return row * (D * 2) + ((c ^ swz<D>(row)) << 4);
-}
-
 __device__ __forceinline__ i16x8 lds_read16(const char GFA_LDS* base, int off) {
   return *reinterpret_cast<const i16x8 GFA_LDS*>(base + off);
 }
@@ -229,35 +223,13 @@ struct TileLoader {
   }
 };
 
-// Partial score block C(32 x 32) = sum_kk A_kk * B_kk over KT k-steps, where A_kk are rows
-// of a swizzled LDS tile (per-lane offsets koff[kk % 8] + 256 * (kk / 8) + extra) and B_kk
-// are register-resident fragments. LDS reads run PF steps ahead of the MFMAs; two
-// independent accumulation chains are summed at the end.
-template <bool IS_BF16, int KT, int PF>
-__device__ __forceinline__ f32x16 mma_chain_lds(const char GFA_LDS* tile, const int (&koff)[8], int extra,
-                                                const i16x8 (&bf)[KT]) {
-  static_assert(KT % 2 == 0 && PF <= KT, "bad chain shape");
-  f32x16 c0 = f32x16{}, c1 = f32x16{};
-  i16x8 a[PF];
-#pragma unroll
-  for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, koff[i & 7] + 256 * (i >> 3) + extra);
-#pragma unroll
-  for (int kk = 0; kk < KT; ++kk) {
-    const i16x8 cur = a[kk % PF];
-    if (kk + PF < KT) a[kk % PF] = lds_read16(tile, koff[(kk + PF) & 7] + 256 * ((kk + PF) >> 3) + extra);
-    if (kk & 1) {
-      c1 = mma32<IS_BF16>(cur, bf[kk], c1);
-    } else {
-      c0 = mma32<IS_BF16>(cur, bf[kk], c0);
-    }
-  }
-  return c0 + c1;
-}
-
-// Single-accumulator variant of mma_chain_lds (back-to-back dependent MFMAs; 16 fewer
-// live registers). With SG != 0 the scheduler is told to keep PF LDS reads in flight:
-// PF reads first, then one read after every MFMA (call it inside its own scheduling
-// region, between two sched_barrier(0)).
+// Score block C(32 x 32) = sum_kk A_kk * B_kk over KT k-steps, where A_kk are rows of a
+// swizzled LDS tile (per-lane offsets koff[kk % 8] + 256 * (kk / 8) + extra) and B_kk are
+// register-resident fragments, as one chain of back-to-back dependent MFMAs (a second,
+// independent chain measured slower and costs 16 live registers). LDS reads run PF steps
+// ahead of the MFMAs. With SG != 0 the scheduler is told to keep PF LDS reads in flight: PF
+// reads first, then one read after every MFMA (call it inside its own scheduling region,
+// between two sched_barrier(0)).
 template <bool IS_BF16, int KT, int PF, int SG = 0>
 __device__ __forceinline__ f32x16 mma_chain1_lds(const char GFA_LDS* tile, const int (&koff)[8], int extra,
                                                  const i16x8 (&bf)[KT]) {
