@@ -1,4 +1,5 @@
-"""GPU parity at the BASELINE sizes (configs 2-4 and the N=16384 headline layer).
+"""GPU parity at the BASELINE sizes (configs 2-4 and the N=16384 headline layer) and at the
+bench's N=16384 D=128 / D=64 workloads.
 
 Two kinds of check:
   * against the oracle's query-chunked torch float32 path (``forward_chunked`` /
@@ -37,6 +38,10 @@ LARGE = {
     "c3_d256_swa1024_16x8_n16k": (1, 16, 8, 16384, 256, True, 1024, torch.bfloat16, 1.0, 8),
     "headline_d512_causal_32x4_n16k": (1, 32, 4, 16384, 512, True, 0, torch.bfloat16, 1.0, 1),
     "c4_d512_causal_16x2_n32k_fp16": (1, 16, 2, 32768, 512, True, 0, torch.float16, 0.5, 1),
+    # the bench's D=128 / D=64 workloads (the rest of the reference's head-dim range)
+    "d128_causal_32x8_n16k": (1, 32, 8, 16384, 128, True, 0, torch.bfloat16, 1.0, 2),
+    "d64_causal_32x32_n16k": (1, 32, 32, 16384, 64, True, 0, torch.bfloat16, 1.0, 4),
+    "d128_swa2048_16x4_n16k_fp16": (1, 16, 4, 16384, 128, True, 2048, torch.float16, 1.0, 4),
 }
 
 
@@ -71,7 +76,8 @@ def test_large_vs_chunked_fp32(name, device):
     assert max(errs) <= GRAD_TOL
 
 
-@pytest.mark.parametrize("name", ["headline_d512_causal_32x4_n16k", "c3_d256_swa1024_16x8_n16k"])
+@pytest.mark.parametrize("name", ["headline_d512_causal_32x4_n16k", "c3_d256_swa1024_16x8_n16k",
+                                  "d128_causal_32x8_n16k", "d64_causal_32x32_n16k"])
 def test_large_invariants(name, device):
     B, Hq, Hkv, N, D, causal, window, dtype, amp, _ = LARGE[name]
     print(f"case {name}", flush=True)
