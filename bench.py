@@ -271,11 +271,10 @@ def measure_traffic(name, calib_mib=1024, timeout_s=180, keep_dir=None):
 # sliding-window layers with head dim 256, window 512, and 7 full-causal layers with head
 # dim 512, the pattern four sliding then one full; GQA 8:1; per-layer input embeddings).
 # Built locally from transformers' Gemma4TextConfig with random weights (no checkpoint).
-E2E_CONFIG = dict(vocab_size=262144, hidden_size=1536, intermediate_size=6144, num_hidden_layers=35,
-                  num_attention_heads=8, num_key_value_heads=1, head_dim=256, global_head_dim=512,
-                  sliding_window=512, hidden_size_per_layer_input=256, vocab_size_per_layer_input=262144,
-                  layer_types=["full_attention" if (i + 1) % 5 == 0 else "sliding_attention" for i in range(35)],
-                  max_position_embeddings=32768)
+def _e2e_config() -> dict:
+    """Config 5's model configuration, committed beside this script."""
+    with open(os.path.join(ROOT, "bench_e2e_config.json")) as f:
+        return json.load(f)["gemma4_text_config"]
 
 
 def bench_e2e(device, seq_len=16384, steps=3, warmup=1):
@@ -288,7 +287,7 @@ def bench_e2e(device, seq_len=16384, steps=3, warmup=1):
 
     print(f"[bench] e2e: Gemma-4-E2B architecture, random init, N={seq_len}", file=sys.stderr, flush=True)
     gfa.register_triton_attention()
-    cfg = Gemma4TextConfig(**E2E_CONFIG)
+    cfg = Gemma4TextConfig(**_e2e_config())
     torch.manual_seed(0)
     with torch.device(device):
         model = Gemma4ForCausalLM(cfg)
@@ -316,8 +315,8 @@ def bench_e2e(device, seq_len=16384, steps=3, warmup=1):
            "peak_hbm_gib": round(peak / 2 ** 30, 3), "weights_gib": round(base / 2 ** 30, 3),
            "params": n_params, "finite": ok, "layers": cfg.num_hidden_layers,
            "attention": "triton_gqa (this engine via register_triton_attention)",
-           "logits": "last position only (logits_to_keep=1)", "config": {k: v for k, v in E2E_CONFIG.items()
-                                                                          if k != "layer_types"},
+           "logits": "last position only (logits_to_keep=1)", "config_file": "bench_e2e_config.json",
+           "config": {k: v for k, v in _e2e_config().items() if k != "layer_types"},
            "layer_pattern": "4 x sliding_attention (D=256, W=512) then 1 x full_attention (D=512), x7"}
     print(f"[bench] e2e: {res['ms']} ms, {res['tokens_per_s']} tok/s, peak {res['peak_hbm_gib']} GiB "
           f"(weights {res['weights_gib']} GiB)", file=sys.stderr, flush=True)
