@@ -10,7 +10,9 @@
  * a unit-stride head dimension and 16-byte aligned rows. lse/delta are float32
  * (B, Hq, lse_ld) with lse_ld >= GFA_LSE_LD(N): the backward kernels read whole query
  * tiles of up to 64 rows, so rows N..lse_ld-1 must exist (their values are never used).
- * Query head h reads KV head h / (Hq / Hkv) (contiguous groups).
+ * Query head h reads KV head h / (Hq / Hkv) (contiguous groups). head_dim is 64, 128, 256
+ * or 512 (the reference documents 64-512, powers of two); anything else returns
+ * GFA_ERR_UNSUPPORTED, as does a (batch, head) slice spanning more than 4 GiB.
  *
  * The entry points replace the reference's Triton launch sites (file:line in
  * /root/reference, zzhhjjj/gemma-triton-flash-attn):
