@@ -76,14 +76,19 @@ def kernel_bytes(w):
             "dkv": 2 * qsz + 4 * kvsz + 2 * rows}         # Q, dO, K, V, LSE, delta in; dK, dV out
 
 
-def make_inputs(w, device):
+def make_inputs(w, device, layout="bhnd"):
+    """q, k, v, dO of the workload. ``layout='bnhd'`` gives (B, H, N, D) views of
+    (B, N, H, D) storage: the strides transformers hands to an attention function."""
     import torch
 
     dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[w["dtype"]]
     g = torch.Generator().manual_seed(0)
     shapes = [(w["B"], w["Hq"], w["N"], w["D"]), (w["B"], w["Hkv"], w["N"], w["D"]),
               (w["B"], w["Hkv"], w["N"], w["D"]), (w["B"], w["Hq"], w["N"], w["D"])]
-    return [(torch.randn(*s, generator=g) * w["amp"]).to(device=device, dtype=dt) for s in shapes]
+    ts = [(torch.randn(*s, generator=g) * w["amp"]).to(device=device, dtype=dt) for s in shapes]
+    if layout == "bnhd":
+        ts = [t.transpose(1, 2).contiguous().transpose(1, 2) for t in ts]
+    return ts
 
 
 def time_loop(fn, iters, warmup):
@@ -101,7 +106,7 @@ def time_loop(fn, iters, warmup):
     return start.elapsed_time(end) / iters
 
 
-def bench_workload(name, w, steps, warmup, device, kernels=True):
+def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd"):
     import torch
 
     import gemma_triton_flash_attn_amd as gfa
@@ -109,8 +114,8 @@ def bench_workload(name, w, steps, warmup, device, kernels=True):
     from gemma_triton_flash_attn_amd.attention import _backward, _forward
 
     print(f"[bench] {name}: {w}", file=sys.stderr, flush=True)
-    q, k, v, do = make_inputs(w, device)
-    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    q, k, v, do = make_inputs(w, device, layout)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))  # clone keeps the strides
     scale = w["D"] ** -0.5
 
     def fwd():
@@ -356,6 +361,8 @@ def main(argv=None):
     ap.add_argument("--copy-calib-mib", type=int, default=1024,
                     help="size of the plain copy that calibrates FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 model forward (Gemma-4-E2B arch)")
+    ap.add_argument("--no-strided", action="store_true",
+                    help="skip the headline run on transformers-style (B, N, H, D)-strided inputs")
     ap.add_argument("--pmc-dir", default=None, help="keep the rocprofv3 counter CSVs in this directory")
     ap.add_argument("--pmc-child", default=None, metavar="WORKLOAD",
                     help="internal: the program profiled by the traffic passes")
@@ -389,6 +396,10 @@ def main(argv=None):
     if head not in results:
         print(json.dumps({"metric": METRIC, "workloads": results}), flush=True)
         return 0
+    if not args.no_strided:
+        # Same step on (B, H, N, D) views of (B, N, H, D) storage, read in place (no copy).
+        results[head + "_hf_strided"] = bench_workload(head + " (B,N,H,D) strides", WORKLOADS[head], args.steps,
+                                                       args.warmup, device, kernels=False, layout="bnhd")
     if args.all:
         for name in ("c2_d512_causal_gqa8_n8k", "c4_d512_causal_gqa8_n32k", "d128_causal_gqa4_n16k",
                      "d64_causal_mha_n16k"):
