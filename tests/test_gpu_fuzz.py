@@ -73,3 +73,50 @@ def test_random_case_vs_oracle(case, device):
     print(f"  O max-abs {err_o:.3e}  dQ/dK/dV rel {errs[0]:.3e} {errs[1]:.3e} {errs[2]:.3e}", flush=True)
     assert err_o <= O_TOL[dtype]
     assert max(errs) <= GRAD_TOL
+
+
+def _mid_cases(n=24, seed=77):
+    """Longer sequences (300-4096): several key/query tiles per window, query splits chosen by
+    the registry for small and mid-size grids, multi-workgroup causal imbalance."""
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        D = rng.choice([64, 128, 256, 512])
+        Hkv = rng.choice([1, 2, 4])
+        R = rng.choice([1, 2, 4, 8])
+        B = rng.choice([1, 1, 2])
+        N = rng.randint(300, 4096 if D <= 256 else 2048)
+        causal = rng.random() < 0.8
+        window = rng.choice([0, rng.randint(2, 300), rng.randint(300, N + 100)]) if causal else 0
+        dtype = rng.choice([torch.float16, torch.bfloat16])
+        layout = rng.choice(["bhnd", "bnhd"])
+        out.append((i, B, Hkv * R, Hkv, N, D, causal, window, dtype, layout))
+    return out
+
+
+@pytest.mark.parametrize("case", _mid_cases(), ids=lambda c: f"m{c[0]}")
+def test_mid_size_case_vs_chunked_oracle(case, device):
+    """Same bar, against the oracle's query-chunked torch fp32 path run on the GPU."""
+    import gemma_triton_flash_attn_amd as gfa
+
+    i, B, Hq, Hkv, N, D, causal, window, dtype, layout = case
+    print(f"case m{i}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal} window={window} {dtype} {layout}",
+          flush=True)
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, dtype, device, seed=5000 + i, layout=layout)
+    qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    o = gfa.flash_attn_gqa_train(qq, kk, vv, causal=causal, slide_size=window)
+    o.backward(do)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = orc.forward_chunked(q, k, v, causal, window)
+    dq_ref, dk_ref, dv_ref, _ = orc.backward_chunked(q, k, v, do, causal, window, o=o_ref, lse=lse_ref)
+    err_o = float((o.detach().float() - o_ref).abs().max())
+
+    def rel(a, b):
+        floor = GRAD_ABS_RMS * b.numel() ** 0.5 / GRAD_TOL
+        return float(torch.linalg.vector_norm(a.float() - b) / max(float(torch.linalg.vector_norm(b)), floor))
+
+    errs = [rel(g, r) for g, r in ((qq.grad, dq_ref), (kk.grad, dk_ref), (vv.grad, dv_ref))]
+    print(f"  O max-abs {err_o:.3e}  dQ/dK/dV rel {errs[0]:.3e} {errs[1]:.3e} {errs[2]:.3e}", flush=True)
+    assert err_o <= O_TOL[dtype]
+    assert max(errs) <= GRAD_TOL
+
