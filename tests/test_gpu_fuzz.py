@@ -3,7 +3,8 @@
 Each case draws (B, Hq, Hkv, N, D, causal, window, dtype, layout, scale) from a fixed seed, so
 the sweep is the same on every run: head dims 64-512, GQA groups 1-16, ragged N up to 300,
 windows from 1 past N, non-causal cases, HF-style strided inputs and a non-default softmax
-scale. The bar is the one in tests/test_gpu_parity.py: O max-abs <= 1e-2 (fp16) / 2e-2
+scale. A second sweep runs longer sequences (N 300-4096) against the oracle's query-chunked
+torch fp32 path on the GPU. The bar is the one in tests/test_gpu_parity.py: O max-abs <= 1e-2 (fp16) / 2e-2
 (bf16), dQ/dK/dV relative Frobenius error <= 5e-2 with an absolute floor for near-zero
 gradients.
 """
