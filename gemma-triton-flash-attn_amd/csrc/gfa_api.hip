@@ -35,20 +35,21 @@ int ok() {
 // dim; dQ: dq_split waves per 32 query rows (2 = a pair splitting the head dim, 1 = one
 // wave over the full head dim); dK/dV: dkv_roles waves per 32 keys (2 = a pair splitting
 // the work by role, P/dV and dS/dK; 1 = one wave doing all four products). NW waves per
-// workgroup.
+// workgroup. fwd_bkv_window is the forward tile used with a sliding window (narrower tiles
+// waste less at the window edge: 8-11% faster at D=128 for windows up to 1024).
 // ---------------------------------------------------------------------------------
 struct Entry {
   int head_dim;
-  int fwd_bkv, fwd_waves;
+  int fwd_bkv, fwd_waves, fwd_bkv_window;
   int dq_bkv, dq_waves, dq_split;
   int dkv_bq, dkv_waves, dkv_roles;
 };
 
 constexpr Entry kRegistry[] = {
-    {512, 32, 4, 32, 4, 2, 32, 4, 2},
-    {256, 32, 4, 32, 4, 1, 32, 4, 1},
-    {128, 64, 4, 32, 4, 1, 32, 4, 2},
-    {64, 64, 4, 32, 4, 1, 32, 4, 1},
+    {512, 32, 4, 32, 32, 4, 2, 32, 4, 2},
+    {256, 32, 4, 32, 32, 4, 1, 32, 4, 1},
+    {128, 64, 4, 32, 32, 4, 1, 32, 4, 2},
+    {64, 64, 4, 64, 32, 4, 1, 32, 4, 1},
 };
 
 const Entry* lookup(int d) {
@@ -180,7 +181,8 @@ int gfa_fwd(const gfa_fwd_args* a) {
   }
   if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
   const Entry* e = lookup(a->head_dim);
-  const int bkv = a->block_kv ? a->block_kv : e->fwd_bkv;
+  const bool windowed = a->causal && a->window > 0 && a->window < a->seq_len;
+  const int bkv = a->block_kv ? a->block_kv : (windowed ? e->fwd_bkv_window : e->fwd_bkv);
   const int nw = e->fwd_waves;
   if (!fwd_built(a->head_dim, bkv, nw))
     return fail(GFA_ERR_UNSUPPORTED, "no forward kernel built for head_dim=%d block_kv=%d", a->head_dim, bkv);

@@ -32,6 +32,7 @@ class KernelConfig:
     dkv_waves: int
     dkv_roles: int      # waves per 32 keys in the dKV kernel (2: role-split pair; 1: one wave)
     fwd_block_kv_options: tuple = ()  # other built forward tile widths (BLOCK_KV override)
+    fwd_block_kv_window: int = 0      # forward tile with a sliding window (0 = fwd_block_kv)
 
 
 REGISTRY: dict[int, KernelConfig] = {
@@ -43,7 +44,7 @@ REGISTRY: dict[int, KernelConfig] = {
                       fwd_block_kv_options=(32, 64)),
     128: KernelConfig(128, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
                       dkv_waves=4, dkv_roles=2,
-                      fwd_block_kv_options=(32, 64)),
+                      fwd_block_kv_options=(32, 64), fwd_block_kv_window=32),
     64: KernelConfig(64, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
                      dkv_waves=4, dkv_roles=1,
                      fwd_block_kv_options=(32, 64)),

@@ -84,3 +84,14 @@ def test_engine_registry_known_answers(shape):
     cfg = gfa.get_config(*shape)
     for key, want in ENGINE_KNOWN[shape].items():
         assert cfg[key] == want, (key, cfg[key], want)
+
+
+def test_windowed_forward_tile():
+    """With a sliding window the D=128 forward runs 32-key tiles (less waste at the window
+    edge); the other head dims keep their default."""
+    from gemma_triton_flash_attn_amd.registry import REGISTRY
+
+    assert REGISTRY[128].fwd_block_kv_window == 32
+    assert all(REGISTRY[d].fwd_block_kv_window in (0, REGISTRY[d].fwd_block_kv) for d in (64, 256, 512))
+    assert all(c.fwd_block_kv_window in (0,) + tuple(c.fwd_block_kv_options) for c in REGISTRY.values())
+
