@@ -9,14 +9,14 @@ computed by hand-written HIP kernels behind a C ABI (include/gfa.h, libgfa.so):
     flash_attn_gqa_op(q, k, v, causal=False, slide_size=0) -> out        same, as torch.library
                                                                          ops gfa::attn_fwd/bwd
                                                                          (torch.compile-able)
-    attention(q, k, v)                                                   non-causal MHA
+    attention(q, k, v)                                                   torch SDPA (reference helper)
     attention_gqa_ref / attention_swa_ref                                torch math references
     register_triton_attention(name="triton_gqa"), triton_gqa_attention   HF integration
     REGISTRY / get_config                                                HEAD_DIM-keyed configs
 
 q: (B, N_Q_HEADS, N, D), k/v: (B, N_KV_HEADS, N, D), fp16/bf16, D in {64, 128, 256, 512}.
 """
-from .attention import FlashAttnGQAFunction, attention, attention_flash_gqa, flash_attn_gqa_train
+from .attention import FlashAttnGQAFunction, attention_flash_gqa, flash_attn_gqa_train
 from .ops import flash_attn_gqa_op
 from .hf_integration import (
     patch_gemma4_shared_kv_states_for_fsdp2,
@@ -24,7 +24,7 @@ from .hf_integration import (
     register_triton_attention,
     triton_gqa_attention,
 )
-from .reference import attention_gqa_ref, attention_swa_ref
+from .reference import attention, attention_gqa_ref, attention_swa_ref
 from .registry import REGISTRY, SUPPORTED_HEAD_DIMS, KernelConfig, get_config
 
 __version__ = "1.0.1"

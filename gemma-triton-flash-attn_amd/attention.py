@@ -5,7 +5,9 @@ Mirrors /root/reference/flash_attn/attention.py:
   * ``FlashAttnGQAFunction``  autograd function: forward stores LSE, backward runs the
                               dQ kernel (fused delta) then the pack-GQA dKV kernel (1433-1622)
   * ``flash_attn_gqa_train``  training entry point (1625-1635)
-  * ``attention``             plain (non-causal, MHA) scaled dot-product attention (11-17)
+
+(The reference's torch helper ``attention`` (11-17) lives in reference.py with the other
+PyTorch reference functions.)
 
 Tensors are (B, H, N, D) with any (batch, head, row) strides and a unit-stride head dim;
 query head h uses KV head h // (Hq // Hkv). ``slide_size`` > 0 with ``causal`` limits query
@@ -227,10 +229,3 @@ def attention_flash_gqa(q, k, v, causal=False, slide_size=0, BLOCK_Q=None, BLOCK
     o, _ = _forward(q, k, v, causal, slide_size, _default_scale(D, scale), store_lse=False, block_kv=bkv)
     return o
 
-
-def attention(q, k, v):
-    """Standard (non-causal, MHA) scaled dot-product attention (reference attention.py:11-17),
-    computed by the same HIP forward kernel."""
-    if q.shape[1] != k.shape[1]:
-        raise ValueError("attention() is the MHA form; use attention_flash_gqa for GQA")
-    return attention_flash_gqa(q, k, v, causal=False)

@@ -29,14 +29,22 @@ def triton_gqa_attention(module, query, key, value, attention_mask, dropout: flo
                          sliding_window: int | None = None, **kwargs):
     """transformers attention-interface adapter: returns ``(out[B, N, Hq, D], None)``.
 
-    ``attention_mask`` is ignored: the kernels build the causal / sliding-window mask from
-    ``module.is_causal`` and ``sliding_window`` (reference 30-76). softcap and non-zero
-    dropout raise NotImplementedError rather than return wrong numerics.
+    The kernels build the causal / sliding-window mask from ``module.is_causal`` and
+    ``sliding_window`` (reference 30-76). ``attention_mask`` is what the mask creator
+    registered beside this function hands over: None when no token is padded. A padding
+    mask with masked positions, a prepared 4-D mask, or packed sequences (``cu_seq_lens_*``
+    keyword arguments) raise NotImplementedError instead of being ignored, as do softcap
+    and non-zero dropout: never wrong numerics.
     """
     if softcap is not None:
         raise NotImplementedError("triton_gqa_attention does not support softcap")
     if dropout != 0.0:
         raise NotImplementedError("triton_gqa_attention does not support dropout")
+    if attention_mask is not None:
+        if attention_mask.dim() != 2 or not bool(attention_mask.all()):
+            raise NotImplementedError("triton_gqa_attention does not support padding or custom attention masks")
+    if kwargs.get("cu_seq_lens_q") is not None or kwargs.get("cu_seq_lens_k") is not None:
+        raise NotImplementedError("triton_gqa_attention does not support packed sequences (cu_seq_lens)")
     scale = scaling if scaling is not None else module.head_dim ** -0.5
     slide = int(sliding_window) if sliding_window else 0
     is_causal = getattr(module, "is_causal", True)
@@ -44,12 +52,34 @@ def triton_gqa_attention(module, query, key, value, attention_mask, dropout: flo
     return out.transpose(1, 2).contiguous(), None
 
 
+def padding_mask_for_engine(batch_size, q_length, kv_length, q_offset=0, kv_offset=0, mask_function=None,
+                            attention_mask=None, **kwargs):
+    """Mask creator registered under the same name as the attention function.
+
+    transformers drops a 2-D padding mask for attention functions that have no mask creator
+    of their own (masking_utils._preprocess_mask_arguments), which would make padded
+    batches silently wrong. This one hands the adapter the (B, kv_length) boolean padding
+    mask when any key is padded, and None otherwise (the kernels build the causal and
+    window masks themselves)."""
+    if attention_mask is None:
+        return None
+    m = attention_mask[:, -kv_length:]
+    if m.shape[1] == kv_length and bool(m.all()):
+        return None
+    return m
+
+
 def register_triton_attention(name: str = "triton_gqa") -> None:
     """Register ``triton_gqa_attention`` under ``name`` in transformers' global attention
-    registry (reference 79-88)."""
+    registry (reference 79-88), with ``padding_mask_for_engine`` as its mask creator."""
     from transformers import AttentionInterface
 
     AttentionInterface.register(name, triton_gqa_attention)
+    try:
+        from transformers.masking_utils import AttentionMaskInterface
+    except ImportError:  # transformers without mask interfaces: masks reach the adapter as given
+        return
+    AttentionMaskInterface.register(name, padding_mask_for_engine)
 
 
 def patch_transformers_5_5_4_flash_attn_key() -> None:

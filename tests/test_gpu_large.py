@@ -6,7 +6,7 @@ Two kinds of check:
     ``backward_chunked``) run on the GPU on the same 16-bit inputs. For the largest shapes
     the reference is restricted to the query heads of KV head 0; the engine still runs
     the whole problem, and those heads' outputs and dK/dV of KV head 0 depend on nothing
-    else;
+    else. The last KV head is compared as well, so both ends of every tensor are covered;
   * size-independent identities that hold for the full problem and need no reference:
       - every output row is a convex combination of V rows: min V <= O <= max V;
       - sum over keys of dV equals the sum of dO over the KV group's query heads (rows of P
@@ -59,21 +59,37 @@ def _engine(q, k, v, do, causal, window):
     return o.detach(), qq.grad, kk.grad, vv.grad
 
 
+def _check_kv_heads(q, k, v, do, o, dq, dk, dv, causal, window, dtype, kv_lo, kv_hi):
+    """Compare the engine's outputs of KV heads [kv_lo, kv_hi) and their query heads with
+    the chunked fp32 oracle run on those heads alone."""
+    R = q.shape[1] // k.shape[1]
+    hq = slice(kv_lo * R, kv_hi * R)
+    hk = slice(kv_lo, kv_hi)
+    o_ref, lse_ref = orc.forward_chunked(q[:, hq], k[:, hk], v[:, hk], causal, window)
+    err_o = float((o[:, hq].float() - o_ref).abs().max())
+    dq_ref, dk_ref, dv_ref, _ = orc.backward_chunked(q[:, hq], k[:, hk], v[:, hk], do[:, hq], causal, window,
+                                                     o=o_ref, lse=lse_ref)
+    errs = (_rel(dq[:, hq], dq_ref), _rel(dk[:, hk], dk_ref), _rel(dv[:, hk], dv_ref))
+    print(f"  KV heads [{kv_lo}, {kv_hi}): O max-abs {err_o:.3e}  dQ/dK/dV rel {errs[0]:.3e} {errs[1]:.3e} "
+          f"{errs[2]:.3e}", flush=True)
+    del o_ref, lse_ref, dq_ref, dk_ref, dv_ref
+    assert err_o <= O_TOL[dtype]
+    assert max(errs) <= GRAD_TOL
+
+
 @pytest.mark.parametrize("name", list(LARGE))
 def test_large_vs_chunked_fp32(name, device):
+    """The first ``ref_kv`` KV heads with their query heads and, where that leaves heads
+    out, the last KV head too (its query heads, LSE rows and dK/dV slices sit at the far
+    end of every tensor)."""
     B, Hq, Hkv, N, D, causal, window, dtype, amp, ref_kv = LARGE[name]
     print(f"case {name}", flush=True)
     q, k, v, do = make_inputs(B, Hq, Hkv, N, D, dtype, device, seed=0, scale=amp)
     o, dq, dk, dv = _engine(q, k, v, do, causal, window)
-    hq = ref_kv * (Hq // Hkv)  # query heads of the first ref_kv KV heads
-    o_ref, lse_ref = orc.forward_chunked(q[:, :hq], k[:, :ref_kv], v[:, :ref_kv], causal, window)
-    err_o = float((o[:, :hq].float() - o_ref).abs().max())
-    dq_ref, dk_ref, dv_ref, _ = orc.backward_chunked(q[:, :hq], k[:, :ref_kv], v[:, :ref_kv], do[:, :hq], causal,
-                                                     window, o=o_ref, lse=lse_ref)
-    errs = (_rel(dq[:, :hq], dq_ref), _rel(dk[:, :ref_kv], dk_ref), _rel(dv[:, :ref_kv], dv_ref))
-    print(f"  O max-abs {err_o:.3e}  dQ/dK/dV rel {errs[0]:.3e} {errs[1]:.3e} {errs[2]:.3e}", flush=True)
-    assert err_o <= O_TOL[dtype]
-    assert max(errs) <= GRAD_TOL
+    _check_kv_heads(q, k, v, do, o, dq, dk, dv, causal, window, dtype, 0, ref_kv)
+    if ref_kv < Hkv:
+        torch.cuda.empty_cache()
+        _check_kv_heads(q, k, v, do, o, dq, dk, dv, causal, window, dtype, Hkv - 1, Hkv)
 
 
 @pytest.mark.parametrize("name", ["headline_d512_causal_32x4_n16k", "c3_d256_swa1024_16x8_n16k",

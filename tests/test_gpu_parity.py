@@ -168,7 +168,8 @@ def test_q_splits_match(qs, D, device):
 
 @pytest.mark.parametrize("dtype,jump,D", [(torch.float16, 16.0, 256), (torch.bfloat16, 60.0, 256),
                                          (torch.float16, 5.0, 256), (torch.float16, 16.0, 128),
-                                         (torch.float16, 16.0, 64)])
+                                         (torch.float16, 16.0, 64), (torch.float16, 16.0, 512),
+                                         (torch.bfloat16, 60.0, 512)])
 def test_late_large_scores(dtype, jump, D, device):
     """Scores that grow far above the first tile's maximum. The forward fixes each row's
     reference max at its first visible tile; rows whose later scores exceed it by more

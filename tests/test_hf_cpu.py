@@ -45,3 +45,50 @@ def test_oracle_attention_matches_sdpa_inside_the_model():
     a = logits_with(model, "gfa_oracle_cpu2", ids)
     b = logits_with(model, "sdpa", ids)
     assert float((a - b).abs().max()) < 1e-3
+
+
+def test_padding_mask_reaches_the_adapter_and_is_refused():
+    """transformers drops a 2-D padding mask for attention functions without a mask creator.
+    register_triton_attention installs one, so a padded batch hands the adapter its padding
+    mask (and an unpadded one hands over None); the adapter refuses masked positions instead
+    of ignoring them."""
+    from types import SimpleNamespace
+
+    from transformers import AttentionInterface
+
+    import gemma_triton_flash_attn_amd as gfa
+
+    seen = []
+
+    def probe(module, query, key, value, attention_mask, **kwargs):
+        seen.append(None if attention_mask is None else attention_mask.clone())
+        o = torch.zeros(query.shape[0], query.shape[2], query.shape[1], query.shape[3], dtype=query.dtype)
+        return o, None
+
+    gfa.register_triton_attention("gfa_mask_probe")
+    AttentionInterface.register("gfa_mask_probe", probe)  # same name: keeps the engine's mask creator
+    cfg = tiny_gemma4_config(n_layers=2, sliding_window=8)
+    model = build_model(cfg, "cpu", torch.float32)
+    ids = torch.randint(0, cfg.vocab_size, (2, 24), generator=torch.Generator().manual_seed(2))
+    pad = torch.ones(2, 24, dtype=torch.long)
+    pad[1, 18:] = 0
+    model.config._attn_implementation = "gfa_mask_probe"
+    for m in model.modules():
+        c = getattr(m, "config", None)
+        if c is not None and hasattr(c, "_attn_implementation"):
+            c._attn_implementation = "gfa_mask_probe"
+    with torch.no_grad():
+        model(input_ids=ids, attention_mask=pad, use_cache=False)
+    assert len(seen) == 2 and all(s is not None and s.shape == (2, 24) for s in seen)
+    assert torch.equal(seen[0].to(torch.long), pad)
+    seen.clear()
+    with torch.no_grad():
+        model(input_ids=ids, attention_mask=torch.ones(2, 24, dtype=torch.long), use_cache=False)
+    assert seen == [None, None]
+
+    mod = SimpleNamespace(head_dim=256, is_causal=True)
+    q = torch.zeros(2, 2, 24, 256)
+    with pytest.raises(NotImplementedError, match="padding"):
+        gfa.triton_gqa_attention(mod, q, q, q, pad.bool())
+    with pytest.raises(NotImplementedError, match="packed"):
+        gfa.triton_gqa_attention(mod, q, q, q, None, cu_seq_lens_q=torch.tensor([0, 10, 24]))

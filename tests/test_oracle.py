@@ -187,3 +187,19 @@ def test_chunked_matches_dense(causal, window):
     dq2, dk2, dv2, delta2 = orc.backward_chunked(tq, tk, tv, tdo, causal, window, chunk=8)
     for a, b in ((o, o2), (lse, lse2), (dq, dq2), (dk, dk2), (dv, dv2), (delta, delta2)):
         np.testing.assert_allclose(b.numpy(), a, atol=2e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("causal,window", [(True, 0), (True, 7), (True, 1), (False, 0), (True, 64)])
+def test_cpu_baseline_restatement_matches_oracle(causal, window):
+    """The function the reported CPU baseline times (oracle/cpu_baseline.py sdpa_math_gqa,
+    the reference's attention_gqa_ref / attention_swa_ref path) computes the same attention
+    as the float64 oracle: GQA expansion, causal and sliding-window masks. A wrong head
+    mapping, a window off by one or a dropped causal flag fails here."""
+    from oracle.cpu_baseline import sdpa_math_gqa
+
+    B, Hq, Hkv, N, D = 2, 8, 2, 29, 16
+    q, k, v = (_rand(s, 40 + i) for i, s in enumerate([(B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D)]))
+    got = sdpa_math_gqa(*(torch.tensor(x, dtype=torch.float32) for x in (q, k, v)), causal=causal, window=window)
+    ref, _ = orc.forward(q, k, v, causal, window)
+    assert got.shape == ref.shape
+    assert float(np.abs(got.double().numpy() - ref).max()) < 2e-5
