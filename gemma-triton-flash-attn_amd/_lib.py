@@ -30,7 +30,9 @@ STATUS_NAMES = {
     4: "GFA_ERR_LAUNCH",
 }
 
-EXPORTED = ("gfa_fwd", "gfa_bwd", "gfa_bwd_workspace_size", "gfa_config", "gfa_last_error", "gfa_version")
+EXPORTED = ("gfa_fwd", "gfa_bwd", "gfa_bwd_noalloc", "gfa_bwd_workspace_size", "gfa_config", "gfa_last_error",
+            "gfa_version")
+NOALLOC_SCRATCH_BYTES = 64 << 20  # GFA_NOALLOC_SCRATCH_BYTES
 
 
 class GfaError(RuntimeError):
@@ -106,6 +108,8 @@ def load() -> ctypes.CDLL:
         lib.gfa_fwd.restype = ctypes.c_int
         lib.gfa_bwd.argtypes = [ctypes.POINTER(BwdArgs)]
         lib.gfa_bwd.restype = ctypes.c_int
+        lib.gfa_bwd_noalloc.argtypes = [ctypes.POINTER(BwdArgs)]
+        lib.gfa_bwd_noalloc.restype = ctypes.c_int
         lib.gfa_bwd_workspace_size.argtypes = [ctypes.c_int32] * 8
         lib.gfa_bwd_workspace_size.restype = ctypes.c_size_t
         lib.gfa_config.argtypes = [ctypes.c_int32] * 5 + [ctypes.POINTER(ConfigInfo)]

@@ -124,9 +124,11 @@ def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bo
 
 
 def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, q_splits: int = 0,
-              stages: int = 0, out=None):
+              stages: int = 0, out=None, noalloc: bool = False):
     """Run gfa_bwd. ``stages`` selects kernels (0 = all; GFA_BWD_DQ / GFA_BWD_DKV bits);
-    ``out`` = (dq, dk, dv, delta) reuses caller buffers (profiling a single stage)."""
+    ``out`` = (dq, dk, dv, delta) reuses caller buffers (profiling a single stage).
+    ``noalloc`` calls gfa_bwd_noalloc instead: delta and the workspace then live in the
+    library's own scratch (the returned delta is None)."""
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     do = _prep(do)
@@ -140,13 +142,14 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
         dv = torch.empty_like(v)
         dq, dk, dv = (t if not _needs_copy(t) else torch.empty(t.shape, dtype=t.dtype, device=t.device)
                       for t in (dq, dk, dv))
-        delta = torch.empty((B, Hq, lse_ld(N)), dtype=torch.float32, device=q.device)
+        delta = None if noalloc else torch.empty((B, Hq, lse_ld(N)), dtype=torch.float32, device=q.device)
     lib = _lib.load()
-    ws_bytes = int(lib.gfa_bwd_workspace_size(B, Hq, Hkv, N, D, int(bool(causal)), int(slide_size), int(q_splits)))
+    ws_bytes = 0 if noalloc else int(lib.gfa_bwd_workspace_size(B, Hq, Hkv, N, D, int(bool(causal)), int(slide_size),
+                                                                 int(q_splits)))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     a = _lib.BwdArgs()
     a.q, a.k, a.v, a.o, a.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr()
-    a.lse, a.delta = lse.data_ptr(), delta.data_ptr()
+    a.lse, a.delta = lse.data_ptr(), (delta.data_ptr() if delta is not None else None)
     a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
     (a.q_strides, a.k_strides, a.v_strides, a.o_strides, a.do_strides, a.dq_strides, a.dk_strides,
      a.dv_strides) = (_lib.strides_of(t) for t in (q, k, v, o, do, dq, dk, dv))
@@ -162,7 +165,7 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
     a.workspace_bytes = ws_bytes
     a.stream = _stream(q.device)
     with torch.cuda.device(q.device):
-        _lib.check(lib.gfa_bwd(ctypes.byref(a)))
+        _lib.check((lib.gfa_bwd_noalloc if noalloc else lib.gfa_bwd)(ctypes.byref(a)))
     return dq, dk, dv, delta
 
 

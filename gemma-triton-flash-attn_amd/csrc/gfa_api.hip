@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/gfa.h"
 #include "gfa_launch.h"
@@ -231,8 +232,14 @@ size_t gfa_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, 
   return (size_t)qs * 2 * batch * heads_kv * (size_t)seq_len * head_dim * sizeof(float);
 }
 
-int gfa_bwd(const gfa_bwd_args* a) {
-  if (a == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "args is NULL");
+}  // extern "C"
+
+namespace {
+
+// Validation and launches of the backward. `delta` and `ws` are the caller's buffers
+// (gfa_bwd) or slices of the library's scratch array (gfa_bwd_noalloc); `qs_in` is the
+// q_splits to use (0 = registry choice).
+int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_bytes, int qs_in) {
   int rc = check_dims(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->dtype, a->window);
   if (rc) return rc;
   if ((rc = check_view("q", a->q, a->q_strides, true))) return rc;
@@ -250,21 +257,21 @@ int gfa_bwd(const gfa_bwd_args* a) {
     for (int i = 0; i < 8; ++i)
       if ((rc = check_span(names[i], *views[i], a->seq_len, a->head_dim))) return rc;
   }
-  if (a->lse == nullptr || a->delta == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "lse and delta are required");
-  if (a->lse_ld < GFA_LSE_LD(a->seq_len) || (a->lse_ld & 3) || !aligned16(a->lse) || !aligned16(a->delta))
+  if (a->lse == nullptr || delta_buf == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "lse and delta are required");
+  if (a->lse_ld < GFA_LSE_LD(a->seq_len) || (a->lse_ld & 3) || !aligned16(a->lse) || !aligned16(delta_buf))
     return fail(GFA_ERR_INVALID_ARGUMENT, "lse_ld=%d must be >= %d (multiple of 4, 16-byte aligned lse/delta)",
                 a->lse_ld, GFA_LSE_LD(a->seq_len));
   if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
   const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
   if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);
   const Entry* e = lookup(a->head_dim);
-  const int qs = a->q_splits > 0 ? a->q_splits : pick_q_splits(a->batch, a->heads_kv, a->seq_len, e->dkv_waves / e->dkv_roles);
+  const int qs = qs_in > 0 ? qs_in : pick_q_splits(a->batch, a->heads_kv, a->seq_len, e->dkv_waves / e->dkv_roles);
   if (qs != 1 && qs != 2 && qs != 4 && qs != 8) return fail(GFA_ERR_INVALID_ARGUMENT, "q_splits=%d not in {1,2,4,8}", qs);
   const size_t need = gfa_bwd_workspace_size(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->causal,
                                              a->window, qs);
-  if (need > 0 && (a->workspace == nullptr || a->workspace_bytes < need))
-    return fail(GFA_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, a->workspace_bytes);
-  if (need > 0 && !aligned16(a->workspace)) return fail(GFA_ERR_INVALID_ARGUMENT, "workspace is not 16-byte aligned");
+  if (need > 0 && (ws_buf == nullptr || ws_bytes < need))
+    return fail(GFA_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, ws_bytes);
+  if (need > 0 && !aligned16(ws_buf)) return fail(GFA_ERR_INVALID_ARGUMENT, "workspace is not 16-byte aligned");
 
   const bool bf16 = a->dtype == GFA_DTYPE_BF16;
   const int R = a->heads_q / a->heads_kv;
@@ -279,7 +286,7 @@ int gfa_bwd(const gfa_bwd_args* a) {
   pq.o = static_cast<const uint16_t*>(a->o);
   pq.dout = static_cast<const uint16_t*>(a->dout);
   pq.lse = a->lse;
-  pq.delta = a->delta;
+  pq.delta = delta_buf;
   pq.dq = static_cast<uint16_t*>(a->dq);
   pq.qv = rv(a->q_strides);
   pq.kv = rv(a->k_strides);
@@ -311,10 +318,10 @@ int gfa_bwd(const gfa_bwd_args* a) {
   pk.v = pq.v;
   pk.dout = pq.dout;
   pk.lse = a->lse;
-  pk.delta = a->delta;
+  pk.delta = delta_buf;
   pk.dk = static_cast<uint16_t*>(a->dk);
   pk.dv = static_cast<uint16_t*>(a->dv);
-  pk.part = static_cast<float*>(a->workspace);
+  pk.part = static_cast<float*>(ws_buf);
   pk.qv = pq.qv;
   pk.kv = pq.kv;
   pk.vv = pq.vv;
@@ -342,6 +349,89 @@ int gfa_bwd(const gfa_bwd_args* a) {
     if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV reduce launch failed: %s", hipGetErrorString(err));
   }
   return ok();
+}
+
+// ---------------------------------------------------------------------------------
+// Library-owned scratch of gfa_bwd_noalloc: the delta rows, then the Q-split fp32 partials.
+// Every GPU the library runs on holds its own copy at its own address until the process
+// ends. In host code `scratch` is only a stand-in for the symbol: its device address comes
+// from hipGetSymbolAddress, taken once per device with that device current.
+// ---------------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[GFA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to (the current device for the
+// null stream).
+int scratch_on(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t err = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "cannot resolve the stream's device: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices) return fail(GFA_ERR_UNSUPPORTED, "device %d beyond the %d the library tracks", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    if ((err = hipGetDevice(&cur)) != hipSuccess)
+      return fail(GFA_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(err));
+    if (cur != dev && (err = hipSetDevice(dev)) != hipSuccess)
+      return fail(GFA_ERR_LAUNCH, "hipSetDevice(%d) failed: %s", dev, hipGetErrorString(err));
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) hipSetDevice(cur);
+    if (err != hipSuccess || p == nullptr)
+      return fail(GFA_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(err));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gfa_bwd(const gfa_bwd_args* a) {
+  if (a == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "args is NULL");
+  return bwd_impl(a, a->delta, a->workspace, a->workspace_bytes, a->q_splits);
+}
+
+int gfa_bwd_noalloc(const gfa_bwd_args* a) {
+  if (a == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->delta != nullptr || a->workspace != nullptr || a->workspace_bytes != 0)
+    return fail(GFA_ERR_INVALID_ARGUMENT,
+                "gfa_bwd_noalloc keeps delta and the workspace in its own scratch: pass delta = NULL, "
+                "workspace = NULL, workspace_bytes = 0");
+  int rc = check_dims(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->dtype, a->window);
+  if (rc) return rc;
+  if (a->lse_ld < GFA_LSE_LD(a->seq_len) || (a->lse_ld & 3))
+    return fail(GFA_ERR_INVALID_ARGUMENT, "lse_ld=%d must be >= %d (multiple of 4)", a->lse_ld, GFA_LSE_LD(a->seq_len));
+  const size_t cap = GFA_NOALLOC_SCRATCH_BYTES;
+  const size_t delta_bytes = ((size_t)a->batch * a->heads_q * a->lse_ld * sizeof(float) + 255) & ~(size_t)255;
+  if (delta_bytes > cap)
+    return fail(GFA_ERR_WORKSPACE, "delta needs %zu bytes; gfa_bwd_noalloc's scratch holds %zu (use gfa_bwd)",
+                delta_bytes, cap);
+  int qs = a->q_splits;
+  if (qs == 0) {
+    // The registry's split count, halved until its partials fit beside delta (1 needs none).
+    const Entry* e = lookup(a->head_dim);
+    qs = pick_q_splits(a->batch, a->heads_kv, a->seq_len, e->dkv_waves / e->dkv_roles);
+    while (qs > 1 && delta_bytes + gfa_bwd_workspace_size(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim,
+                                                          a->causal, a->window, qs) > cap)
+      qs /= 2;
+  }
+  if (qs != 1 && qs != 2 && qs != 4 && qs != 8) return fail(GFA_ERR_INVALID_ARGUMENT, "q_splits=%d not in {1,2,4,8}", qs);
+  const size_t ws = gfa_bwd_workspace_size(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->causal,
+                                           a->window, qs);
+  if (delta_bytes + ws > cap)
+    return fail(GFA_ERR_WORKSPACE,
+                "q_splits=%d needs %zu scratch bytes (delta %zu + partials %zu); gfa_bwd_noalloc holds %zu "
+                "(use q_splits=0 or gfa_bwd)", qs, delta_bytes + ws, delta_bytes, ws, cap);
+  void* base = nullptr;
+  if ((rc = scratch_on(static_cast<hipStream_t>(a->stream), &base))) return rc;
+  char* p = static_cast<char*>(base);
+  return bwd_impl(a, reinterpret_cast<float*>(p), ws ? p + delta_bytes : nullptr, ws, qs);
 }
 
 }  // extern "C"

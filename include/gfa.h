@@ -127,6 +127,23 @@ int gfa_fwd(const gfa_fwd_args* args);
 /* Backward: delta, dQ, then dK/dV (summing Q-split fp32 partials when q_splits > 1). */
 int gfa_bwd(const gfa_bwd_args* args);
 
+/* Bytes of the library-owned device scratch of gfa_bwd_noalloc, per GPU. */
+#define GFA_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* gfa_bwd without caller-provided scratch. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving or training
+ * loops, harnesses that forbid hipMalloc). The caller passes inputs and outputs only: delta
+ * and workspace must be NULL and workspace_bytes 0. delta and the Q-split partials live in a
+ * file-scope device array of GFA_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds
+ * until the process ends; the call itself allocates nothing. delta takes
+ * batch * heads_q * lse_ld * 4 bytes (rounded up to 256) and the partials
+ * gfa_bwd_workspace_size(...) bytes: a request beyond the scratch returns GFA_ERR_WORKSPACE.
+ * q_splits = 0 takes the registry's split count, halved until its partials fit (1 needs none).
+ * Every call on one GPU shares that GPU's scratch and leaves its contents there (a later
+ * stages = GFA_BWD_DKV call reads the delta of the last GFA_BWD_DQ call): calls that overlap
+ * on one GPU (concurrent streams or threads) race. Otherwise as gfa_bwd. */
+int gfa_bwd_noalloc(const gfa_bwd_args* args);
+
 /* Workspace bytes gfa_bwd needs for the given problem and q_splits (0 = registry choice). */
 size_t gfa_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len, int32_t head_dim,
                               int32_t causal, int32_t window, int32_t q_splits);

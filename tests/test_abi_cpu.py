@@ -217,3 +217,35 @@ def test_grid_larger_than_one_launch_is_rejected():
     assert lib.gfa_fwd(ctypes.byref(a)) == 2
     assert b"launch grid" in lib.gfa_last_error()
 
+
+@fake_pointers
+def test_bwd_noalloc_rejects_caller_scratch_and_oversize():
+    """gfa_bwd_noalloc takes inputs and outputs only, and refuses requests whose delta (or
+    explicit Q-split partials) exceed its fixed scratch, before touching any device."""
+    lib = _lib.load()
+    a = _lib.BwdArgs()
+    for name in ("q", "k", "v", "o", "dout", "dq", "dk", "dv"):
+        setattr(a, name, 256)
+    a.lse = 512
+    for s in ("q_strides", "k_strides", "v_strides", "o_strides", "do_strides", "dq_strides", "dk_strides",
+              "dv_strides"):
+        setattr(a, s, _lib.Strides(8 * 64 * 512, 64 * 512, 512))
+    a.batch, a.heads_q, a.heads_kv, a.seq_len, a.head_dim = 1, 8, 1, 64, 512
+    a.causal, a.scale, a.dtype, a.lse_ld = 1, 512 ** -0.5, _lib.GFA_DTYPE_BF16, 64
+    a.delta = 1024  # caller scratch is not accepted
+    assert lib.gfa_bwd_noalloc(ctypes.byref(a)) == 1
+    assert b"NULL" in lib.gfa_last_error()
+    a.delta = None
+    a.workspace, a.workspace_bytes = 4096, 1 << 20
+    assert lib.gfa_bwd_noalloc(ctypes.byref(a)) == 1
+    a.workspace, a.workspace_bytes = None, 0
+    # delta of 2^25 rows x 4 bytes = 128 MiB > 64 MiB scratch
+    a.batch, a.heads_q, a.heads_kv, a.seq_len = 512, 64, 64, 1024
+    a.lse_ld = 1024
+    assert lib.gfa_bwd_noalloc(ctypes.byref(a)) == 3
+    assert b"scratch" in lib.gfa_last_error()
+    # explicit q_splits whose partials do not fit: 8 x 2 x 4 x 8192 x 512 x 4 B = 512 MiB
+    a.batch, a.heads_q, a.heads_kv, a.seq_len, a.lse_ld = 1, 32, 4, 8192, 8192
+    a.q_splits = 8
+    assert lib.gfa_bwd_noalloc(ctypes.byref(a)) == 3
+    assert lib.gfa_bwd_noalloc(None) == 1

@@ -1,0 +1,97 @@
+"""gfa_bwd_noalloc, the backward entry point that allocates nothing: delta and the Q-split
+partials live in the library's own device scratch instead of caller buffers.
+
+Checked through the C ABI against gfa_bwd on the same inputs: at the same q_splits the
+two must agree bit for bit (same kernels, same fixed-order reduction), on two calls in a
+row where the second is smaller than the first (the scratch keeps the first call's
+contents, which must not leak into the second). Where the scratch makes the automatic
+split count smaller than gfa_bwd's, the results must still agree to the north-star bar
+(gradients within 5e-2 relative), and the explicit-split form must again be bitwise.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+GRAD_TOL = 5e-2
+
+
+def _rel(a, b):
+    return float(torch.linalg.vector_norm(a.float() - b.float()) / torch.linalg.vector_norm(b.float()))
+
+
+def _grads(q, k, v, do, causal, window, noalloc, q_splits=0):
+    from gemma_triton_flash_attn_amd.attention import _backward, _forward
+
+    scale = q.shape[-1] ** -0.5
+    o, lse = _forward(q, k, v, causal, window, scale, store_lse=True)
+    dq, dk, dv, delta = _backward(q, k, v, o, lse, do, causal, window, scale, q_splits=q_splits, noalloc=noalloc)
+    torch.cuda.synchronize()
+    assert (delta is None) == noalloc
+    return dq, dk, dv
+
+
+# Pairs of calls: (B, Hq, Hkv, N, D, causal, window, dtype, q_splits), the second smaller.
+PAIRS = {
+    "d512_causal": [(1, 8, 2, 1000, 512, True, 0, torch.bfloat16, 1), (1, 4, 1, 300, 512, True, 0, torch.bfloat16, 1)],
+    "d256_swa": [(2, 16, 8, 2048, 256, True, 256, torch.bfloat16, 0), (1, 4, 2, 130, 256, True, 64, torch.float16, 0)],
+    "split_partials": [(1, 8, 1, 2048, 512, True, 0, torch.bfloat16, 4), (1, 4, 2, 200, 128, False, 0, torch.float16, 2)],
+    "d64_split8": [(2, 8, 8, 777, 64, True, 100, torch.bfloat16, 8), (1, 2, 1, 65, 64, True, 0, torch.bfloat16, 2)],
+}
+
+
+def _noalloc_splits(B, Hq, Hkv, N, D, causal, window):
+    """The split count gfa_bwd_noalloc picks for q_splits = 0 (include/gfa.h): the
+    registry's, halved until its partials fit beside delta in the scratch."""
+    from gemma_triton_flash_attn_amd import _lib
+    from gemma_triton_flash_attn_amd.attention import lse_ld
+
+    delta = (B * Hq * lse_ld(N) * 4 + 255) // 256 * 256
+    qs = _lib.config(B, Hq, Hkv, N, D)["q_splits"]
+    while qs > 1 and delta + _lib.bwd_workspace_size(B, Hq, Hkv, N, D, causal, window, qs) > _lib.NOALLOC_SCRATCH_BYTES:
+        qs //= 2
+    return qs
+
+
+@pytest.mark.parametrize("name", list(PAIRS))
+def test_noalloc_matches_gfa_bwd_bitwise(name, device):
+    """Same split count on both sides (for q_splits = 0, the one gfa_bwd_noalloc picks)."""
+    for i, (B, Hq, Hkv, N, D, causal, window, dtype, qs) in enumerate(PAIRS[name]):
+        ref_qs = qs or _noalloc_splits(B, Hq, Hkv, N, D, causal, window)
+        print(f"case {name} call {i}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal} window={window} "
+              f"{dtype} q_splits={qs} (gfa_bwd at {ref_qs})", flush=True)
+        q, k, v, do = make_inputs(B, Hq, Hkv, N, D, dtype, device, seed=100 + i)
+        ref = _grads(q, k, v, do, causal, window, noalloc=False, q_splits=ref_qs)
+        got = _grads(q, k, v, do, causal, window, noalloc=True, q_splits=qs)
+        for name_, a, b in zip(("dq", "dk", "dv"), got, ref):
+            assert torch.equal(a, b), f"{name_} differs from gfa_bwd"
+        if qs == 0:  # and to the north-star bar against gfa_bwd's own choice
+            for a, b in zip(got, _grads(q, k, v, do, causal, window, noalloc=False)):
+                assert _rel(a, b) <= GRAD_TOL
+
+
+def test_noalloc_auto_split_fits_the_scratch(device):
+    """B1 8:1 N=2048 D=512: the registry asks for 8 splits (64 MiB of partials), which do
+    not fit beside delta in the 64 MiB scratch, so gfa_bwd_noalloc runs 4. Equal bit for bit
+    to gfa_bwd at 4 splits, and to the north-star bar against gfa_bwd's own choice."""
+    from gemma_triton_flash_attn_amd import _lib
+
+    B, Hq, Hkv, N, D = 1, 8, 1, 2048, 512
+    assert _lib.config(B, Hq, Hkv, N, D)["q_splits"] == 8
+    assert _lib.bwd_workspace_size(B, Hq, Hkv, N, D, True, 0, 8) >= _lib.NOALLOC_SCRATCH_BYTES
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, torch.bfloat16, device, seed=7)
+    auto = _grads(q, k, v, do, True, 0, noalloc=True)
+    four = _grads(q, k, v, do, True, 0, noalloc=False, q_splits=4)
+    eight = _grads(q, k, v, do, True, 0, noalloc=False)
+    for a, b in zip(auto, four):
+        assert torch.equal(a, b)
+    for a, b in zip(auto, eight):
+        assert _rel(a, b) <= GRAD_TOL
+    # a smaller call right after, reusing the scratch
+    q, k, v, do = make_inputs(1, 2, 1, 96, 512, torch.bfloat16, device, seed=8)
+    for a, b in zip(_grads(q, k, v, do, True, 0, noalloc=True), _grads(q, k, v, do, True, 0, noalloc=False)):
+        assert torch.equal(a, b)
