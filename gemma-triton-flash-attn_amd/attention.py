@@ -30,9 +30,11 @@ from .registry import lookup
 _DTYPES = {torch.float16: _lib.GFA_DTYPE_FP16, torch.bfloat16: _lib.GFA_DTYPE_BF16}
 
 
-# One (batch, head) slice must span at most 4 GiB: the kernels address tiles through 32-bit
-# buffer offsets (gfa_api.hip, check_span).
+# One (batch, head) slice, plus the rows a tile copy may address past its end, must span at
+# most 4 GiB: the kernels address tiles through 32-bit buffer offsets (gfa_api.hip,
+# check_span).
 _SLICE_LIMIT = 0xFFFFFFFF
+_TILE_OVERRUN = 128
 
 
 def _layout_ok(t: torch.Tensor) -> bool:
@@ -40,7 +42,7 @@ def _layout_ok(t: torch.Tensor) -> bool:
     of 8 elements, and one (batch, head) slice within the 4 GiB buffer range."""
     s = t.stride()
     return (s[3] == 1 and all(x % 8 == 0 and x >= 0 for x in s[:3])
-            and ((t.shape[2] - 1) * s[2] + t.shape[3]) * t.element_size() <= _SLICE_LIMIT)
+            and ((t.shape[2] - 1 + _TILE_OVERRUN) * s[2] + t.shape[3]) * t.element_size() <= _SLICE_LIMIT)
 
 
 def _needs_copy(t: torch.Tensor) -> bool:

@@ -8,7 +8,7 @@
 #include <cstring>
 #include <mutex>
 
-#include "../../include/gfa.h"
+#include "gfa.h"
 #include "gfa_launch.h"
 #include "gfa_params.h"
 
@@ -43,14 +43,14 @@ struct Entry {
   int head_dim;
   int fwd_bkv, fwd_waves, fwd_bkv_window;
   int dq_bkv, dq_waves, dq_split;
-  int dkv_bq, dkv_waves, dkv_roles;
+  int dkv_bq, dkv_waves, dkv_roles, dkv_wgs_per_cu;
 };
 
 constexpr Entry kRegistry[] = {
-    {512, 32, 4, 32, 32, 4, 2, 32, 4, 2},
-    {256, 32, 4, 32, 32, 4, 1, 32, 4, 1},
-    {128, 64, 4, 32, 32, 4, 1, 32, 4, 2},
-    {64, 64, 4, 64, 32, 4, 1, 32, 4, 1},
+    {512, 32, 4, 32, 32, 4, 2, 32, 4, 2, 1},
+    {256, 32, 4, 32, 32, 4, 1, 32, 4, 1, 1},
+    {128, 64, 4, 32, 32, 4, 1, 32, 4, 2, 2},
+    {64, 64, 4, 64, 32, 4, 1, 32, 4, 1, 2},
 };
 
 const Entry* lookup(int d) {
@@ -81,20 +81,33 @@ gfa::QGrid make_qgrid(int B, int Hkv, int R, int N, int nu) {
   return g;
 }
 
-// Smallest of {1, 2, 4, 8} giving at least four dK/dV workgroups per CU (256 CUs on MI355X):
-// below that, splitting the query range beats the cost of the fp32 partials (measured from
-// 64 to 1024 key-grid workgroups at D = 64..512). units = 32-key units per workgroup.
-int pick_q_splits(int B, int Hkv, int N, int units) {
+// Smallest of {1, 2, 4, 8} that fills the GPU with dK/dV workgroups: `rounds` rounds of
+// 256 CUs x wgs_per_cu resident workgroups. A full-causal grid needs two rounds: its key
+// blocks carry unequal work, which the heaviest-first grid order balances once there are
+// two rounds or more; windowed and non-causal grids have near-uniform work and need one.
+// Beyond that a split only adds fp32 partial traffic (measured on grids of 32 to 1024
+// workgroups at D = 64..512, causal, windowed and full). units = 32-key units per workgroup.
+int pick_q_splits(int B, int Hkv, int N, int units, int wgs_per_cu, bool full_causal) {
   const int keys_per_wg = 32 * units;
-  const int grid = ((N + keys_per_wg - 1) / keys_per_wg) * B * Hkv;
+  const long long grid = (long long)((N + keys_per_wg - 1) / keys_per_wg) * B * Hkv;
+  const long long want = (full_causal ? 2 : 1) * 256LL * wgs_per_cu;
   int qs = 1;
-  while (qs < 8 && grid * qs < 4 * 256) qs *= 2;
+  while (qs < 8 && grid * qs < want) qs *= 2;
   return qs;
+}
+
+int pick_q_splits(const Entry* e, int B, int Hkv, int N, int causal, int window) {
+  const bool windowed = causal && window > 0 && window < N;
+  return pick_q_splits(B, Hkv, N, e->dkv_waves / e->dkv_roles, e->dkv_wgs_per_cu, causal && !windowed);
 }
 
 gfa::RowView rv(const gfa_strides& s) { return gfa::RowView{s.batch, s.head, s.row}; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Rows past the end of a slice that a tile copy may address (largest tile 64 rows, and a
+// loop's last prefetch starts at most one tile past the last row).
+constexpr int kTileOverrun = 128;
 
 int check_view(const char* name, const void* ptr, const gfa_strides& s, bool need_ptr) {
   if (need_ptr && ptr == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "%s is NULL", name);
@@ -108,9 +121,11 @@ int check_view(const char* name, const void* ptr, const gfa_strides& s, bool nee
 
 // The kernels move tiles with buffer instructions whose record count and offsets are 32-bit,
 // one buffer resource per (batch, head) slice, so one slice (N rows at the row stride) must
-// fit in 4 GiB. Contiguous (B, H, N, D) tensors reach that only at N * D > 2^31.
+// fit in 4 GiB. The last tile of a loop also addresses up to 127 rows past the sequence end
+// (the range check turns them into zeros), and those offsets must not wrap either.
+// Contiguous (B, H, N, D) tensors reach the limit only at (N + 127) * D > 2^31.
 int check_span(const char* name, const gfa_strides& s, int N, int D) {
-  const long long span = ((long long)(N - 1) * s.row + D) * 2;
+  const long long span = ((long long)(N - 1 + kTileOverrun) * s.row + D) * 2;
   if (span > 0xFFFFFFFFll)
     return fail(GFA_ERR_UNSUPPORTED,
                 "%s: one (batch, head) slice spans %lld bytes; the tile copies address at most 4 GiB per slice "
@@ -162,7 +177,7 @@ int gfa_config(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len
   out->dkv_block_kv = 32 * (e->dkv_waves / e->dkv_roles);
   out->dkv_block_q = e->dkv_bq;
   out->dkv_waves = e->dkv_waves;
-  out->q_splits = pick_q_splits(batch, heads_kv, seq_len, e->dkv_waves / e->dkv_roles);
+  out->q_splits = pick_q_splits(e, batch, heads_kv, seq_len, 1, 0);
   return ok();
 }
 
@@ -223,11 +238,9 @@ int gfa_fwd(const gfa_fwd_args* a) {
 size_t gfa_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len, int32_t head_dim,
                               int32_t causal, int32_t window, int32_t q_splits) {
   (void)heads_q;
-  (void)causal;
-  (void)window;
   const Entry* e = lookup(head_dim);
   if (e == nullptr || batch <= 0 || heads_kv <= 0 || seq_len <= 0) return 0;
-  const int qs = q_splits > 0 ? q_splits : pick_q_splits(batch, heads_kv, seq_len, e->dkv_waves / e->dkv_roles);
+  const int qs = q_splits > 0 ? q_splits : pick_q_splits(e, batch, heads_kv, seq_len, causal, window);
   if (qs <= 1) return 0;
   return (size_t)qs * 2 * batch * heads_kv * (size_t)seq_len * head_dim * sizeof(float);
 }
@@ -265,7 +278,7 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
   if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);
   const Entry* e = lookup(a->head_dim);
-  const int qs = qs_in > 0 ? qs_in : pick_q_splits(a->batch, a->heads_kv, a->seq_len, e->dkv_waves / e->dkv_roles);
+  const int qs = qs_in > 0 ? qs_in : pick_q_splits(e, a->batch, a->heads_kv, a->seq_len, a->causal, a->window);
   if (qs != 1 && qs != 2 && qs != 4 && qs != 8) return fail(GFA_ERR_INVALID_ARGUMENT, "q_splits=%d not in {1,2,4,8}", qs);
   const size_t need = gfa_bwd_workspace_size(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->causal,
                                              a->window, qs);
@@ -341,7 +354,7 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   pk.lse_ld = a->lse_ld;
   const int keys_per_wg = 32 * (e->dkv_waves / e->dkv_roles);
   pk.n_kb = (pk.N + keys_per_wg - 1) / keys_per_wg;
-  pk.nblocks = pk.n_kb * pk.B * pk.Hkv * qs;
+  pk.nblocks = (pk.n_kb + 3) / 4 * 4 * pk.B * pk.Hkv * qs;  // key blocks in groups of four (bwd_dkv_kernel)
   err = gfa::launch_bwd_dkv(pk, a->head_dim, e->dkv_bq, e->dkv_waves, e->dkv_roles, bf16, stream);
   if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV launch failed: %s", hipGetErrorString(err));
   if (qs > 1) {
@@ -416,7 +429,7 @@ int gfa_bwd_noalloc(const gfa_bwd_args* a) {
   if (qs == 0) {
     // The registry's split count, halved until its partials fit beside delta (1 needs none).
     const Entry* e = lookup(a->head_dim);
-    qs = pick_q_splits(a->batch, a->heads_kv, a->seq_len, e->dkv_waves / e->dkv_roles);
+    qs = pick_q_splits(e, a->batch, a->heads_kv, a->seq_len, a->causal, a->window);
     while (qs > 1 && delta_bytes + gfa_bwd_workspace_size(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim,
                                                           a->causal, a->window, qs) > cap)
       qs /= 2;

@@ -59,14 +59,23 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   const int l32 = lane & 31;
   char GFA_LDS* px = smem + 4 * TILE + unit * PX + lane * 16;
 
-  // ---- workgroup -> (split, b, kv head, key block); early key blocks (most work) first ----
+  // ---- workgroup -> (key block, split, b, kv head) ----
+  // Heaviest first: under causal masking the early key blocks own the longest query
+  // ranges, so groups of four adjacent key blocks are the slowest-varying index (a
+  // key-block-fastest order mixes heavy and light blocks in every round: 1.5x the balanced
+  // makespan on a 512-workgroup grid). Each group of four key blocks of one (split, b, kv
+  // head) is four consecutive logical ids, which xcd_remap places on one XCD: they read the
+  // same query tiles and share them in L2. Ids past the last key block have no work.
   int lid = xcd_remap(blockIdx.x, p.nblocks, 4);
-  const int kb = lid % p.n_kb;
-  lid /= p.n_kb;
+  const int kb_lo = lid & 3;
+  lid >>= 2;
   const int kvh = lid % p.Hkv;
   lid /= p.Hkv;
   const int b = lid % p.B;
-  const int split = lid / p.B;
+  lid /= p.B;
+  const int split = lid % p.q_splits;
+  const int kb = (lid / p.q_splits) * 4 + kb_lo;
+  if (kb >= p.n_kb) return;  // whole workgroup, before any barrier
 
   const int wg_k0 = kb * NU * 32;
   const int wg_k_last = min(p.N, wg_k0 + NU * 32) - 1;

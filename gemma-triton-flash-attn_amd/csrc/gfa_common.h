@@ -256,6 +256,75 @@ __device__ __forceinline__ f32x16 mma_chain1_lds(const char GFA_LDS* tile, const
   return c;
 }
 
+// Per-lane LDS offsets of the k-steps of a score chain, from one base register. The row read
+// by k-step kk sits at chunk (2 * kk + h) ^ swz(row); the swizzle XORs the low chunk bits with a
+// per-row constant, and the k-step only moves chunk bits 1..3 (kk & 7) and whole 256-byte groups
+// (kk >> 3), so offset(kk) = offset(0) ^ ((kk & 7) << 5) + 256 * (kk >> 3): the row term is a
+// multiple of 2 * D >= 128 bytes and never overlaps bits 5..6 (D = 64) or 5..7 (D >= 128).
+// `opaque` hides the base from loop-invariant code motion, so the XORs are recomputed next to
+// their reads (one VALU op each) instead of being hoisted into eight live registers.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+__device__ __forceinline__ int kstep_off(int base, int kk) { return (base ^ ((kk & 7) << 5)) + 256 * (kk >> 3); }
+
+// mma_chain1_lds with the k-step offsets derived from one base (kstep_off).
+template <bool IS_BF16, int KT, int PF, int SG = 0>
+__device__ __forceinline__ f32x16 mma_chain1_lds_b(const char GFA_LDS* tile, int koff0, int extra,
+                                                   const i16x8 (&bf)[KT]) {
+  static_assert(PF <= KT, "bad chain shape");
+  const int kb = opaque(koff0) + extra;
+  f32x16 c = f32x16{};
+  i16x8 a[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, kstep_off(kb, i));
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const i16x8 cur = a[kk % PF];
+    if (kk + PF < KT) a[kk % PF] = lds_read16(tile, kstep_off(kb, kk + PF));
+    c = mma32<IS_BF16>(cur, bf[kk], c);
+  }
+  if constexpr (SG) {
+    __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+#pragma unroll
+    for (int kk = 0; kk < KT - PF; ++kk) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
+  }
+  return c;
+}
+
+// mma_chain1_lds_b with NL tile-copy instructions spread over the chain (as mma_chain1_lds_ld).
+template <bool IS_BF16, int KT, int PF, int NL, typename LD>
+__device__ __forceinline__ f32x16 mma_chain1_lds_ld_b(const char GFA_LDS* tile, int koff0, int extra,
+                                                      const i16x8 (&bf)[KT], LD&& ld) {
+  static_assert(PF <= KT && NL >= 1 && KT % NL == 0, "bad chain shape");
+  constexpr int EV = KT / NL;
+  const int kb = opaque(koff0) + extra;
+  f32x16 c = f32x16{};
+  i16x8 a[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, kstep_off(kb, i));
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const i16x8 cur = a[kk % PF];
+    if (kk + PF < KT) a[kk % PF] = lds_read16(tile, kstep_off(kb, kk + PF));
+    c = mma32<IS_BF16>(cur, bf[kk], c);
+    if (kk % EV == 0) ld(kk / EV);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (kk + PF < KT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if (kk % EV == 0) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+  }
+  return c;
+}
+
 // mma_chain1_lds with NL tile-copy instructions ld(0..NL-1) spread over the chain, one after
 // every KT / NL MFMAs. A wave issues in order and the copies of all its workgroup's waves
 // share the CU's texture path (each copy instruction moves 1 KB), so a run of copy issues
@@ -318,6 +387,44 @@ __device__ __forceinline__ void mma_tr_accumulate(f32x16 (&acc)[DB], const char 
       a[i % PF] = tr_frag(tile, offA[db2 & 3], offB[db2 & 3], ks2 * 16 * (2 * D) + 256 * (db2 >> 2));
     }
     acc[db] = mma32<IS_BF16>(cur, bop[ks], acc[db]);
+  }
+  if constexpr (SG) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);
+#pragma unroll
+    for (int i = 0; i < N - PF; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
+  }
+}
+
+// Transposed-read offsets from one base: the A fragment of column block db (< 4) is read at
+// base_a ^ (db << 6) (rows 4h + t/4) and base_b ^ (db << 6) (8 rows further down), where
+// base_b = (base_a ^ 32) + 16 * D: the swizzle of a row 8 further differs in chunk bit 1 only.
+// Same reasoning as kstep_off: the column block moves chunk bits 2..3, the swizzle XORs them
+// with a per-row constant, and the row and half-chunk terms never overlap bits 5..7.
+template <bool IS_BF16, int D, int DB, int NKS, int PF, int SG = 0>
+__device__ __forceinline__ void mma_tr_accumulate_b(f32x16 (&acc)[DB], const char GFA_LDS* tile, int offA0,
+                                                    const i16x8 (&bop)[NKS]) {
+  constexpr int N = NKS * DB;
+  static_assert(PF <= N, "prefetch deeper than the product count");
+  const int a0 = opaque(offA0);
+  const int b0 = (a0 ^ 32) + 16 * D;
+  auto frag = [&](int i) __attribute__((always_inline)) {
+    const int ks = i / DB, db = i % DB;
+    const int x = (db & 3) << 6;
+    return tr_frag(tile, a0 ^ x, b0 ^ x, ks * 16 * (2 * D) + 256 * (db >> 2));
+  };
+  i16x8 a[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) a[i] = frag(i);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int db = i % DB;
+    const i16x8 cur = a[i % PF];
+    if (i + PF < N) a[i % PF] = frag(i + PF);
+    acc[db] = mma32<IS_BF16>(cur, bop[i / DB], acc[db]);
   }
   if constexpr (SG) {
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);

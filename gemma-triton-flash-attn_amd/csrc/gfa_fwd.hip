@@ -103,7 +103,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     if (swa) all_lo = q0 + 31 - p.window + 1;
   }
   const int q = q0 + l32;
-  const VisRange vis = keys_of_query(q, p.N, p.causal, p.window);
 
   // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole kernel ----
   i16x8 qf[KT];
@@ -114,23 +113,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     for (int kk = 0; kk < KT; ++kk) qf[kk] = *reinterpret_cast<const i16x8*>(qr + 16 * kk);
   }
 
-  // Per-lane LDS byte offsets inside a tile. The swizzle only touches the low 4 bits of
-  // the 16-byte chunk index, so chunk groups of 16 differ by a constant 256 bytes.
-  int koff[8];  // K row l32, chunk 2*kk + h  (+256 * (kk >> 3))
-#pragma unroll
-  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4);
-  int voffA[4], voffB[4];  // V read transposed: rows 4h + t/4 (+8), columns 32*db + ...
+  // Per-lane LDS byte offsets inside a tile, one base each (kstep_off and
+  // mma_tr_accumulate_b derive the others with an XOR next to each read).
+  const int koff0 = l32 * (2 * D) + ((h ^ swz<D>(l32)) << 4);  // K row l32, chunk h (k-step 0)
+  int voff0;  // V read transposed: rows 4h + t/4, column block 0
   {
     const int t16 = lane & 15;
     const int half16 = (lane >> 4) & 1;
     const int rA = 4 * h + (t16 >> 2);
-    const int rB = rA + 8;
-#pragma unroll
-    for (int dl = 0; dl < 4; ++dl) {
-      const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
-      voffA[dl] = rA * (2 * D) + ((c ^ swz<D>(rA)) << 4) + (t16 & 1) * 8;
-      voffB[dl] = rB * (2 * D) + ((c ^ swz<D>(rB)) << 4) + (t16 & 1) * 8;
-    }
+    const int c = 2 * half16 + ((t16 >> 1) & 1);
+    voff0 = rA * (2 * D) + ((c ^ swz<D>(rA)) << 4) + (t16 & 1) * 8;
   }
 
   const uint16_t* kbase = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh;
@@ -157,7 +149,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     const int rn = min(t + 1, t_hi - 1) * BKV;
     const int k0 = t * BKV;
     f32x16 s[SB];
-    s[0] = mma_chain1_lds_ld<IS_BF16, KT, PF, 2 * NI>(kt, koff, 0, qf, [&](int i) {
+    s[0] = mma_chain1_lds_ld_b<IS_BF16, KT, PF, 2 * NI>(kt, koff0, 0, qf, [&](int i) {
       if (i < NI) {
         kload.load_part(i, rn, kn);
       } else {
@@ -165,11 +157,14 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
       }
     });
 #pragma unroll
-    for (int sb = 1; sb < SB; ++sb) s[sb] = mma_chain1_lds<IS_BF16, KT, 4>(kt, koff, sb * 32 * (2 * D), qf);
+    for (int sb = 1; sb < SB; ++sb) s[sb] = mma_chain1_lds_b<IS_BF16, KT, 4>(kt, koff0, sb * 32 * (2 * D), qf);
     __builtin_amdgcn_sched_barrier(0);
 
     const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
     if (need_mask) {
+      // Rebuilt from the lane id on the (few) boundary tiles rather than held in two
+      // registers for the whole kernel.
+      const VisRange vis = keys_of_query(q0 + opaque(l32), p.N, p.causal, p.window);
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
@@ -206,7 +201,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     }
     // O^T += V^T P^T with a fixed read-ahead pipeline; the softmax above shares the
     // scheduling region, so its VALU work can fill the MFMA shadow.
-    mma_tr_accumulate<IS_BF16, D, DB, BKV / 16, 2, 1>(acc, vt, voffA, voffB, pb);
+    mma_tr_accumulate_b<IS_BF16, D, DB, BKV / 16, 2, 1>(acc, vt, voff0, pb);
     __builtin_amdgcn_sched_barrier(0);
     // One wave per SIMD (D >= 256): keep O^T in AGPRs across iterations (the VGPRs hold Q
     // and the working set). With several waves per SIMD (D <= 128) everything fits the
@@ -277,6 +272,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
 GFA_FWD_INST(512, 32, 4, 1)
 GFA_FWD_INST(256, 64, 4, 1)
 GFA_FWD_INST(256, 32, 4, 1)
+GFA_FWD_INST(256, 32, 4, 2)
 GFA_FWD_INST(128, 64, 4, 2)
 GFA_FWD_INST(128, 32, 4, 2)
 GFA_FWD_INST(64, 64, 4, 3)
@@ -298,7 +294,7 @@ hipError_t launch_fwd(const FwdParams& p, int D, int bkv, int nw, bool bf16, hip
   }
   GFA_FWD_CASE(512, 32, 4, 1)
   GFA_FWD_CASE(256, 64, 4, 1)
-  GFA_FWD_CASE(256, 32, 4, 1)
+  GFA_FWD_CASE(256, 32, 4, 2)
   GFA_FWD_CASE(128, 64, 4, 2)
   GFA_FWD_CASE(128, 32, 4, 2)
   GFA_FWD_CASE(64, 64, 4, 3)

@@ -72,7 +72,7 @@ struct BwdDkvParams {
   int q_splits;
   int lse_ld;
   int n_kb;          // number of key blocks (each WKV keys wide)
-  int nblocks;
+  int nblocks;       // q_splits * B * Hkv * n_kb rounded up to whole groups of four key blocks
 };
 
 }  // namespace gfa

@@ -31,6 +31,7 @@ class KernelConfig:
     dkv_block_q: int    # queries per LDS tile in the dKV kernel
     dkv_waves: int
     dkv_roles: int      # waves per 32 keys in the dKV kernel (2: role-split pair; 1: one wave)
+    dkv_wgs_per_cu: int = 1  # dKV workgroups resident per CU (waves per SIMD)
     fwd_block_kv_options: tuple = ()  # other built forward tile widths (BLOCK_KV override)
     fwd_block_kv_window: int = 0      # forward tile with a sliding window (0 = fwd_block_kv)
 
@@ -44,9 +45,9 @@ REGISTRY: dict[int, KernelConfig] = {
                       fwd_block_kv_options=(32, 64)),
     128: KernelConfig(128, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
                       dkv_waves=4, dkv_roles=2,
-                      fwd_block_kv_options=(32, 64), fwd_block_kv_window=32),
+                      dkv_wgs_per_cu=2, fwd_block_kv_options=(32, 64), fwd_block_kv_window=32),
     64: KernelConfig(64, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
-                     dkv_waves=4, dkv_roles=1,
+                     dkv_waves=4, dkv_roles=1, dkv_wgs_per_cu=2,
                      fwd_block_kv_options=(32, 64)),
 }
 
@@ -82,21 +83,34 @@ def query_grid(batch: int, heads_q: int, heads_kv: int, seq_len: int, units: int
             "nblocks": n_qsb * batch * heads_kv * (r // hpw)}
 
 
-def q_splits_for(batch: int, heads_kv: int, seq_len: int, units: int) -> int:
-    """Smallest of {1, 2, 4, 8} giving at least four dKV workgroups per CU (``units`` = 32-key
-    units per workgroup).
+def q_splits_for(batch: int, heads_kv: int, seq_len: int, units: int, wgs_per_cu: int = 1,
+                 full_causal: bool = True) -> int:
+    """Smallest of {1, 2, 4, 8} that fills the GPU with dKV workgroups (``units`` = 32-key
+    units per workgroup, ``wgs_per_cu`` = workgroups resident per CU).
 
     Same intent as the reference's Q_SPLITS rule (attention.py:1576-1587): split each key
-    block's query range only when the raw grid is small. The threshold of four rounds of
-    workgroups is where splitting stopped paying on MI355X (key grids of 64 to 1024
-    workgroups, D = 64..512).
+    block's query range only when the raw grid is small. A full-causal grid asks for two
+    rounds of NUM_CUS * wgs_per_cu workgroups (its key blocks carry unequal work, which the
+    kernel's heaviest-first grid order balances once there are two rounds); windowed and
+    non-causal grids have near-uniform work and ask for one. Measured on MI355X on grids of
+    32 to 1024 workgroups at D = 64..512; beyond that a split only adds fp32 partial traffic.
     """
     keys_per_wg = 32 * units
     grid = -(-seq_len // keys_per_wg) * batch * heads_kv
+    want = (2 if full_causal else 1) * NUM_CUS * wgs_per_cu
     qs = 1
-    while qs < 8 and grid * qs < 4 * NUM_CUS:
+    while qs < 8 and grid * qs < want:
         qs *= 2
     return qs
+
+
+def q_splits_for_problem(batch: int, heads_kv: int, seq_len: int, head_dim: int, causal: bool = True,
+                         window: int = 0) -> int:
+    """The split count gfa_bwd uses (q_splits = 0) for one problem."""
+    c = lookup(head_dim)
+    windowed = causal and 0 < window < seq_len
+    return q_splits_for(batch, heads_kv, seq_len, c.dkv_waves // c.dkv_roles, c.dkv_wgs_per_cu,
+                        causal and not windowed)
 
 
 def get_config(batch: int, heads_q: int, heads_kv: int, seq_len: int, head_dim: int) -> dict:
@@ -115,5 +129,5 @@ def get_config(batch: int, heads_q: int, heads_kv: int, seq_len: int, head_dim: 
         "dkv_block_kv": 32 * (c.dkv_waves // c.dkv_roles),
         "dkv_block_q": c.dkv_block_q,
         "dkv_waves": c.dkv_waves,
-        "q_splits": q_splits_for(batch, heads_kv, seq_len, c.dkv_waves // c.dkv_roles),
+        "q_splits": q_splits_for_problem(batch, heads_kv, seq_len, head_dim, True, 0),
     }

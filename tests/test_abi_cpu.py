@@ -190,7 +190,7 @@ def test_register_into_transformers():
 @fake_pointers
 def test_slice_span_over_4gib_is_rejected():
     """One (batch, head) slice at the row stride must fit the kernels' 32-bit buffer range:
-    HF's (B, N, H, D) layout with 32 heads of 512 at N = 2^17 + 1 spans just over 4 GiB."""
+    HF's (B, N, H, D) layout with 32 heads of 512 at N = 2^17 + 1 spans over 4 GiB."""
     lib = _lib.load()
     n, row = 131073, 32 * 512
     a = _fwd_args(seq_len=n, lse_ld=(n + 63) // 64 * 64, q_strides=_lib.Strides(n * row, 512, row))

@@ -56,7 +56,7 @@ ENGINE_KNOWN = {
     (1, 32, 4, 16384, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
                                  q_splits=1),
     (1, 32, 4, 8192, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
-                                q_splits=2),   # 512-workgroup key grid: under four per CU
+                                q_splits=1),   # 512-workgroup key grid: two rounds of one per CU
     (1, 16, 2, 32768, 512): dict(fwd_block_q=32, fwd_block_kv=32, dq_block_q=32, dkv_block_kv=64, dkv_block_q=32,
                                  q_splits=1),
     (1, 16, 8, 16384, 256): dict(fwd_block_q=64, fwd_block_kv=32, dq_block_q=64, dkv_block_kv=128, dkv_block_q=32,
@@ -84,6 +84,23 @@ def test_engine_registry_known_answers(shape):
     cfg = gfa.get_config(*shape)
     for key, want in ENGINE_KNOWN[shape].items():
         assert cfg[key] == want, (key, cfg[key], want)
+
+
+def test_query_split_rule_by_mask_kind():
+    """Full-causal key grids ask for two rounds of workgroups (unequal work per key block),
+    windowed and non-causal ones for one; D=128 / D=64 keep two dK/dV workgroups per CU."""
+    from gemma_triton_flash_attn_amd.registry import q_splits_for_problem as qs
+
+    # D=256 16:8 N=4096: a 256-workgroup key grid
+    assert qs(1, 8, 4096, 256, causal=True, window=0) == 2
+    assert qs(1, 8, 4096, 256, causal=True, window=1024) == 1
+    assert qs(1, 8, 4096, 256, causal=False) == 1
+    assert qs(1, 8, 4096, 256, causal=True, window=4096) == 2  # a window covering N is plain causal
+    # D=128 8:1 N=16384 W=1024: 256 workgroups, two per CU -> one round needs 512
+    assert qs(1, 1, 16384, 128, causal=True, window=1024) == 2
+    # D=64 16:2 N=8192: 128 workgroups of 128 keys; full causal asks for 2 x 256 x 2
+    assert qs(1, 2, 8192, 64, causal=True) == 8
+    assert qs(1, 4, 8192, 64, causal=True, window=1024) == 2
 
 
 def test_windowed_forward_tile():
