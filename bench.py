@@ -91,11 +91,28 @@ def make_inputs(w, device, layout="bhnd"):
     return ts
 
 
-def time_loop(fn, iters, warmup):
+def time_loop(fn, iters, warmup, min_warm_ms=0.0, min_time_ms=0.0):
+    """Average ms per call of ``fn`` over ``iters`` timed calls after ``warmup`` untimed ones,
+    HIP events on the current stream. With ``min_warm_ms`` / ``min_time_ms`` the warmup and
+    the timed window are extended to at least that much GPU time (sub-millisecond layers:
+    MI355X's clock settles over tens of milliseconds of work, and a few calls would time the
+    ramp rather than the steady state)."""
     import torch
 
     for _ in range(warmup):
         fn()
+    if min_warm_ms or min_time_ms:
+        torch.cuda.synchronize()
+        s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(3):
+            fn()
+        e0.record()
+        torch.cuda.synchronize()
+        per = max(s0.elapsed_time(e0) / 3, 1e-3)
+        for _ in range(int(min_warm_ms / per)):
+            fn()
+        iters = max(iters, int(math.ceil(min_time_ms / per)))
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
@@ -106,7 +123,10 @@ def time_loop(fn, iters, warmup):
     return start.elapsed_time(end) / iters
 
 
-def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd"):
+def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd", exact=False):
+    """Time one workload. ``exact``: the fwd and fwd+bwd loops run exactly ``warmup`` untimed
+    and ``steps`` timed steps (the headline ``value``); otherwise, and for the per-kernel
+    loops, warmup and timed window are extended to at least 100 and 200 ms of GPU time."""
     import torch
 
     import gemma_triton_flash_attn_amd as gfa
@@ -127,9 +147,11 @@ def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd"):
         o.backward(do)
 
     res = {}
+    ext = {} if exact else {"min_warm_ms": 100.0, "min_time_ms": 200.0}
+    kext = {"min_warm_ms": 100.0, "min_time_ms": 200.0}
     with torch.no_grad():
-        ms_fwd = time_loop(lambda: fwd(), steps, warmup)
-    ms_fb = time_loop(fwd_bwd, steps, warmup)
+        ms_fwd = time_loop(lambda: fwd(), steps, warmup, **ext)
+    ms_fb = time_loop(fwd_bwd, steps, warmup, **ext)
     res["ms_fwd"] = ms_fwd
     res["ms_fwd_bwd"] = ms_fb
     res["tflops_fwd"] = charged_flops(w, "fwd") / ms_fwd / 1e9
@@ -144,11 +166,12 @@ def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd"):
         delta = torch.empty(lse.shape, dtype=torch.float32, device=device)
         bufs = (dq, dk, dv, delta)
         per = {
-            "fwd": time_loop(lambda: _forward(q, k, v, w["causal"], w["window"], scale, store_lse=True), steps, 1),
+            "fwd": time_loop(lambda: _forward(q, k, v, w["causal"], w["window"], scale, store_lse=True), steps, 1,
+                             **kext),
             "dq": time_loop(lambda: _backward(q, k, v, o, lse, do, w["causal"], w["window"], scale,
-                                              stages=_lib.GFA_BWD_DQ, out=bufs), steps, 1),
+                                              stages=_lib.GFA_BWD_DQ, out=bufs), steps, 1, **kext),
             "dkv": time_loop(lambda: _backward(q, k, v, o, lse, do, w["causal"], w["window"], scale,
-                                               stages=_lib.GFA_BWD_DKV, out=bufs), steps, 1),
+                                               stages=_lib.GFA_BWD_DKV, out=bufs), steps, 1, **kext),
         }
         kf = kernel_flops(w)
         res["kernels"] = {kname: {"ms": ms, "tflops": kf[kname] / ms / 1e9,
@@ -456,15 +479,15 @@ def main(argv=None):
             return 2
     results = {}
     for n in names:
-        steps = args.steps if n != "d256_swa1024_gqa2_n16k" else max(args.steps, 50)  # sub-ms steps: a longer window
-        results[n] = bench_workload(n, WORKLOADS[n], steps, args.warmup, device, kernels=not args.no_kernels)
+        results[n] = bench_workload(n, WORKLOADS[n], args.steps, args.warmup, device, kernels=not args.no_kernels,
+                                    exact=(n == head))
     if head not in results:
         print(json.dumps({"metric": METRIC, "workloads": results}), flush=True)
         return 0
     if not args.no_strided:
         # Same step on (B, H, N, D) views of (B, N, H, D) storage, read in place (no copy).
         results[head + "_hf_strided"] = bench_workload(head + " (B,N,H,D) strides", WORKLOADS[head], args.steps,
-                                                       args.warmup, device, kernels=False, layout="bnhd")
+                                                       args.warmup, device, kernels=False, layout="bnhd", exact=True)
     if args.all:
         for name in ("d128_causal_gqa4_n16k", "d64_causal_mha_n16k"):
             if name not in results:

@@ -13,10 +13,14 @@ computed by hand-written HIP kernels behind a C ABI (include/gfa.h, libgfa.so):
     attention_gqa_ref / attention_swa_ref                                torch math references
     register_triton_attention(name="triton_gqa"), triton_gqa_attention   HF integration
     REGISTRY / get_config                                                HEAD_DIM-keyed configs
+    segments.from_padding_mask / from_lengths / from_cu_seqlens / from_position_ids
+                                                                         ragged-batch tables
+                                                                         (``segments=`` keyword)
 
 q: (B, N_Q_HEADS, N, D), k/v: (B, N_KV_HEADS, N, D), fp16/bf16, D in {64, 128, 256, 512}.
 """
 from .attention import FlashAttnGQAFunction, attention_flash_gqa, flash_attn_gqa_train
+from . import segments
 from .ops import flash_attn_gqa_op
 from .hf_integration import (
     patch_gemma4_shared_kv_states_for_fsdp2,
@@ -45,5 +49,6 @@ __all__ = [
     "SUPPORTED_HEAD_DIMS",
     "KernelConfig",
     "get_config",
+    "segments",
     "__version__",
 ]

@@ -56,7 +56,7 @@ class FwdArgs(ctypes.Structure):
         ("seq_len", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("causal", ctypes.c_int32), ("window", ctypes.c_int32), ("scale", ctypes.c_float),
         ("dtype", ctypes.c_int32), ("block_kv", ctypes.c_int32), ("lse_ld", ctypes.c_int32),
-        ("stream", ctypes.c_void_p),
+        ("stream", ctypes.c_void_p), ("seg_lo", ctypes.c_void_p), ("seg_hi", ctypes.c_void_p),
     ]
 
 
@@ -74,7 +74,7 @@ class BwdArgs(ctypes.Structure):
         ("dtype", ctypes.c_int32), ("q_splits", ctypes.c_int32), ("lse_ld", ctypes.c_int32),
         ("stages", ctypes.c_int32),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
-        ("stream", ctypes.c_void_p),
+        ("stream", ctypes.c_void_p), ("seg_lo", ctypes.c_void_p), ("seg_hi", ctypes.c_void_p),
     ]
 
 

@@ -14,6 +14,12 @@ query head h uses KV head h // (Hq // Hkv). ``slide_size`` > 0 with ``causal`` l
 i to keys in [i - slide_size + 1, i]; a window is ignored when not causal and a window
 covering the whole sequence is plain causal (reference 1441-1443).
 
+``segments`` (keyword, optional) is a pair of int32 (B, N) tables for variable-length,
+padded or packed batches (segments.py builds them from padding masks, lengths, cu_seqlens or
+position ids): token t attends, and is attended by, only keys [lo[b, t], hi[b, t]) on top of
+the causal / window rule; padding tokens (empty segments) get zero outputs and gradients.
+The reference has no such input (README.md:255-262 lists varlen and padding as unsupported).
+
 Every call goes through libgfa.so's C ABI on the caller's current HIP stream. There is no
 CPU or PyTorch fallback: unsupported inputs raise before anything is launched.
 """
@@ -76,6 +82,23 @@ def _check_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise ValueError("empty sequence or batch")
 
 
+def _check_segments(segments, q: torch.Tensor):
+    """(lo, hi) int32 tables of shape (B, N) on q's device, made contiguous; None passes."""
+    if segments is None:
+        return None
+    if len(segments) != 2:
+        raise ValueError("segments must be a pair (lo, hi) of (B, N) int32 tensors")
+    B, _, N, _ = q.shape
+    out = []
+    for t in segments:
+        if not isinstance(t, torch.Tensor) or tuple(t.shape) != (B, N):
+            raise ValueError(f"segment tables must be (B, N) = {(B, N)} tensors")
+        if t.device != q.device:
+            raise ValueError("segment tables must be on q's device")
+        out.append(t.to(torch.int32).contiguous())
+    return tuple(out)
+
+
 def _norm_window(causal: bool, slide_size: int, n: int) -> int:
     """attention.py:1441-1443: a window covering the whole sequence is plain causal.
     The library ignores the window when not causal (reference kernel 289-293)."""
@@ -99,7 +122,8 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
-def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bool, block_kv: int = 0):
+def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bool, block_kv: int = 0,
+             segments=None):
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     q, k, v = _prep(q), _prep(k), _prep(v)
@@ -120,13 +144,15 @@ def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bo
     a.block_kv = int(block_kv)
     a.lse_ld = ld
     a.stream = _stream(q.device)
+    if segments is not None:
+        a.seg_lo, a.seg_hi = segments[0].data_ptr(), segments[1].data_ptr()
     with torch.cuda.device(q.device):
         _lib.check(_lib.load().gfa_fwd(ctypes.byref(a)))
     return o, lse  # lse is (B, Hq, lse_ld(N)); rows >= N are padding
 
 
 def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, q_splits: int = 0,
-              stages: int = 0, out=None, noalloc: bool = False):
+              stages: int = 0, out=None, noalloc: bool = False, segments=None):
     """Run gfa_bwd. ``stages`` selects kernels (0 = all; GFA_BWD_DQ / GFA_BWD_DKV bits);
     ``out`` = (dq, dk, dv, delta) reuses caller buffers (profiling a single stage).
     ``noalloc`` calls gfa_bwd_noalloc instead: delta and the workspace then live in the
@@ -166,6 +192,8 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
     a.workspace = ws.data_ptr() if ws is not None else None
     a.workspace_bytes = ws_bytes
     a.stream = _stream(q.device)
+    if segments is not None:
+        a.seg_lo, a.seg_hi = segments[0].data_ptr(), segments[1].data_ptr()
     with torch.cuda.device(q.device):
         _lib.check((lib.gfa_bwd_noalloc if noalloc else lib.gfa_bwd)(ctypes.byref(a)))
     return dq, dk, dv, delta
@@ -178,17 +206,22 @@ def _default_scale(d: int, scale: float | None) -> float:
 class FlashAttnGQAFunction(torch.autograd.Function):
     """Autograd function of the GQA flash attention (reference attention.py:1433-1622).
 
-    forward(q, k, v, causal, slide_size, scale=None) -> O; saves q, k, v, O and the fp32 LSE.
-    backward(dO) -> dQ, dK, dV via gfa_bwd (dQ kernel with fused delta, then pack-GQA dKV).
+    forward(q, k, v, causal, slide_size, scale=None, segments=None) -> O; saves q, k, v, O,
+    the fp32 LSE and the segment tables. backward(dO) -> dQ, dK, dV via gfa_bwd (dQ kernel
+    with fused delta, then pack-GQA dKV).
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, causal=False, slide_size=0, scale=None):
+    def forward(ctx, q, k, v, causal=False, slide_size=0, scale=None, segments=None):
         _check_inputs(q, k, v)
+        segments = _check_segments(segments, q)
         slide_size = _norm_window(causal, slide_size, q.shape[2])
         sc = _default_scale(q.shape[3], scale)
-        o, lse = _forward(q, k, v, causal, slide_size, sc, store_lse=True)
-        ctx.save_for_backward(q, k, v, o, lse)
+        o, lse = _forward(q, k, v, causal, slide_size, sc, store_lse=True, segments=segments)
+        if segments is None:
+            ctx.save_for_backward(q, k, v, o, lse)
+        else:
+            ctx.save_for_backward(q, k, v, o, lse, *segments)
         ctx.causal = bool(causal)
         ctx.slide_size = slide_size
         ctx.scale = sc
@@ -196,23 +229,25 @@ class FlashAttnGQAFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do):
-        q, k, v, o, lse = ctx.saved_tensors
+        q, k, v, o, lse, *seg = ctx.saved_tensors
         q, k, v = _prep(q), _prep(k), _prep(v)
-        dq, dk, dv, _ = _backward(q, k, v, o, lse, do, ctx.causal, ctx.slide_size, ctx.scale)
-        return dq, dk, dv, None, None, None
+        dq, dk, dv, _ = _backward(q, k, v, o, lse, do, ctx.causal, ctx.slide_size, ctx.scale,
+                                  segments=tuple(seg) if seg else None)
+        return dq, dk, dv, None, None, None, None
 
 
-def flash_attn_gqa_train(q, k, v, causal=False, slide_size=0, *, scale=None):
+def flash_attn_gqa_train(q, k, v, causal=False, slide_size=0, *, scale=None, segments=None):
     """Flash attention with autograd support (reference attention.py:1625-1635).
 
     q: (B, N_Q_HEADS, N, D); k, v: (B, N_KV_HEADS, N, D); fp16 or bf16; D in {64, 128, 256, 512}.
     ``scale`` defaults to 1/sqrt(D) like the reference; other values are used natively.
+    ``segments``: optional (lo, hi) int32 (B, N) tables for ragged batches (segments.py).
     """
-    return FlashAttnGQAFunction.apply(q, k, v, causal, slide_size, scale)
+    return FlashAttnGQAFunction.apply(q, k, v, causal, slide_size, scale, segments)
 
 
 def attention_flash_gqa(q, k, v, causal=False, slide_size=0, BLOCK_Q=None, BLOCK_KV=None, BLOCK_D=None,
-                        num_warps=None, num_stages=None, *, scale=None):
+                        num_warps=None, num_stages=None, *, scale=None, segments=None):
     """Inference forward without LSE (reference attention.py:540-604). Default causal=False.
 
     ``BLOCK_KV`` selects one of the built LDS tile widths for this head dim. ``BLOCK_Q``,
@@ -231,6 +266,7 @@ def attention_flash_gqa(q, k, v, causal=False, slide_size=0, BLOCK_Q=None, BLOCK
     if BLOCK_D is not None and int(BLOCK_D) != D:
         raise ValueError("BLOCK_D must equal HEAD_DIM (no head-dim tiling)")
     slide_size = _norm_window(causal, slide_size, q.shape[2])
-    o, _ = _forward(q, k, v, causal, slide_size, _default_scale(D, scale), store_lse=False, block_kv=bkv)
+    o, _ = _forward(q, k, v, causal, slide_size, _default_scale(D, scale), store_lse=False, block_kv=bkv,
+                    segments=_check_segments(segments, q))
     return o
 

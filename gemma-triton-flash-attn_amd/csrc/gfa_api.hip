@@ -134,6 +134,13 @@ int check_span(const char* name, const gfa_strides& s, int N, int D) {
   return GFA_OK;
 }
 
+int check_segments(const int32_t* lo, const int32_t* hi) {
+  if ((lo == nullptr) != (hi == nullptr)) return fail(GFA_ERR_INVALID_ARGUMENT, "seg_lo and seg_hi go together");
+  if (lo && ((reinterpret_cast<uintptr_t>(lo) & 3u) || (reinterpret_cast<uintptr_t>(hi) & 3u)))
+    return fail(GFA_ERR_INVALID_ARGUMENT, "segment tables must be 4-byte aligned");
+  return GFA_OK;
+}
+
 int check_dims(int B, int Hq, int Hkv, int N, int D, int dtype, int window) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || N <= 0)
     return fail(GFA_ERR_INVALID_ARGUMENT, "empty problem: B=%d Hq=%d Hkv=%d N=%d", B, Hq, Hkv, N);
@@ -196,6 +203,7 @@ int gfa_fwd(const gfa_fwd_args* a) {
       if ((rc = check_span(names[i], *views[i], a->seq_len, a->head_dim))) return rc;
   }
   if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
+  if ((rc = check_segments(a->seg_lo, a->seg_hi))) return rc;
   const Entry* e = lookup(a->head_dim);
   const bool windowed = a->causal && a->window > 0 && a->window < a->seq_len;
   const int bkv = a->block_kv ? a->block_kv : (windowed ? e->fwd_bkv_window : e->fwd_bkv);
@@ -204,6 +212,8 @@ int gfa_fwd(const gfa_fwd_args* a) {
     return fail(GFA_ERR_UNSUPPORTED, "no forward kernel built for head_dim=%d block_kv=%d", a->head_dim, bkv);
 
   gfa::FwdParams p;
+  p.seg_lo = a->seg_lo;
+  p.seg_hi = a->seg_hi;
   p.q = static_cast<const uint16_t*>(a->q);
   p.k = static_cast<const uint16_t*>(a->k);
   p.v = static_cast<const uint16_t*>(a->v);
@@ -275,6 +285,7 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
     return fail(GFA_ERR_INVALID_ARGUMENT, "lse_ld=%d must be >= %d (multiple of 4, 16-byte aligned lse/delta)",
                 a->lse_ld, GFA_LSE_LD(a->seq_len));
   if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
+  if ((rc = check_segments(a->seg_lo, a->seg_hi))) return rc;
   const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
   if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);
   const Entry* e = lookup(a->head_dim);
@@ -293,6 +304,8 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   hipStream_t stream = static_cast<hipStream_t>(a->stream);
 
   gfa::BwdDqParams pq;
+  pq.seg_lo = a->seg_lo;
+  pq.seg_hi = a->seg_hi;
   pq.q = static_cast<const uint16_t*>(a->q);
   pq.k = static_cast<const uint16_t*>(a->k);
   pq.v = static_cast<const uint16_t*>(a->v);
@@ -326,6 +339,8 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   if (!(stages & GFA_BWD_DKV)) return ok();
 
   gfa::BwdDkvParams pk;
+  pk.seg_lo = a->seg_lo;
+  pk.seg_hi = a->seg_hi;
   pk.q = pq.q;
   pk.k = pq.k;
   pk.v = pq.v;

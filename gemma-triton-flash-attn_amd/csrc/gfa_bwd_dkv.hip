@@ -84,7 +84,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   const int k_last = k0 + 31;
   const int key = k0 + l32;
   const int krow = min(key, p.N - 1);
-  const VisRange vis = queries_of_key(key, p.N, p.causal, p.window);
+  VisRange vis = queries_of_key(key, p.N, p.causal, p.window);
 
   const bool swa = p.causal && p.window > 0;
   // Query tiles the workgroup visits.
@@ -92,6 +92,14 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   if (p.causal) {
     qt_lo = wg_k0 / BQ;
     if (swa) qt_hi = min(qt_hi, (wg_k_last + p.window - 1) / BQ + 1);
+  }
+  // Segment table (optional): a key serves the queries of its own segment only.
+  const int* slo = p.seg_lo ? p.seg_lo + (int64_t)b * p.N : nullptr;
+  const int* shi = p.seg_lo ? p.seg_hi + (int64_t)b * p.N : nullptr;
+  if (slo) {
+    qt_lo = max(qt_lo, clamp_n(slo[wg_k0], p.N) / BQ);
+    qt_hi = min(qt_hi, (clamp_n(shi[wg_k_last], p.N) + BQ - 1) / BQ);
+    vis = intersect(vis, clamp_n(slo[krow], p.N), clamp_n(shi[krow], p.N));
   }
   const int nqt = max(0, qt_hi - qt_lo);
   const int total = p.R * nqt;
@@ -104,6 +112,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   if (p.causal) {
     all_lo = k_last;
     if (swa) all_hi = min(p.N, k0 + p.window);  // q - key < window for the first key
+  }
+  if (slo && active) {
+    all_lo = max(all_lo, clamp_n(slo[min(k_last, p.N - 1)], p.N));
+    all_hi = min(all_hi, clamp_n(shi[k0], p.N));
   }
   const bool pair_full = k_last < p.N;
 

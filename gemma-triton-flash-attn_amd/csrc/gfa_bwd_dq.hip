@@ -78,6 +78,14 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     k_hi = wg_q_hi;
     if (swa) k_lo = max(0, wg_q_lo - p.window + 1);
   }
+  // Segment table (optional): the workgroup's queries see keys from the first query's
+  // segment start to the last query's segment end (both rows are non-decreasing).
+  const int* slo = p.seg_lo ? p.seg_lo + (int64_t)b * p.N : nullptr;
+  const int* shi = p.seg_lo ? p.seg_hi + (int64_t)b * p.N : nullptr;
+  if (slo) {
+    k_lo = max(k_lo, clamp_n(slo[wg_q_lo], p.N));
+    k_hi = min(k_hi, clamp_n(shi[wg_q_hi - 1], p.N));
+  }
   const int t_lo = k_lo / BKV;
   // Even tile count (the loop is unrolled by two): an odd range gets one extra tile past
   // the workgroup's keys, which is fully masked (dS = 0; zero-filled past the sequence end).
@@ -93,7 +101,14 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 
   const int q = q0 + l32;
   const int qrow = min(q, p.N - 1);
-  const VisRange vis = keys_of_query(q, p.N, p.causal, p.window);
+  VisRange vis = keys_of_query(q, p.N, p.causal, p.window);
+  if (slo) {
+    if (active) {
+      all_lo = max(all_lo, clamp_n(slo[min(q_last, p.N - 1)], p.N));
+      all_hi = min(all_hi, clamp_n(shi[q0], p.N));
+    }
+    vis = intersect(vis, clamp_n(slo[qrow], p.N), clamp_n(shi[qrow], p.N));
+  }
   // ---- Q and dO halves (B operands), resident; delta prologue ----
   i16x8 qf[KTH], df[KTH];
   float dpart = 0.f;

@@ -103,6 +103,19 @@ __device__ __forceinline__ VisRange queries_of_key(int k, int n, int causal, int
   return make_range(lo, hi);
 }
 
+// Segment tables (optional): token t of a batch row attends and is attended only within
+// keys [lo[t], hi[t]); an empty segment (lo == hi) marks a token that takes part in nothing
+// (padding). Both rows are non-decreasing in t. Table values are clamped to [0, n], so any
+// table content keeps every tile range inside the sequence.
+__device__ __forceinline__ int clamp_n(int x, int n) { return min(max(x, 0), n); }
+
+// [v] intersected with keys (or queries) [lo, hi).
+__device__ __forceinline__ VisRange intersect(VisRange v, int lo, int hi) {
+  const int b0 = max(v.base, lo);
+  const int e0 = min(v.base + (int)v.width, hi - 1);
+  return make_range(b0, e0);
+}
+
 // Keep a kernel-lifetime MFMA operand fragment in AGPRs. MFMA reads A/B operands from
 // AGPRs directly; left alone, the allocator keeps such fragments in the 256 arch VGPRs
 // and spills once the fp32 accumulators fill the AGPR file.

@@ -36,7 +36,7 @@
 
 namespace gfa {
 
-template <int D, int BKV, bool IS_BF16, int NW, int WPE>
+template <int D, int BKV, bool IS_BF16, int NW, int WPE, bool SEG>
 __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   constexpr int KT = D / 16;   // MFMA k-steps over the head dim
   constexpr int DB = D / 32;   // 32-row blocks of the O^T accumulator
@@ -90,9 +90,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     k_hi = wg_q_hi;
     if (swa) k_lo = max(0, wg_q_lo - p.window + 1);
   }
+  // Segment table (SEG): the workgroup's queries see keys from the first query's segment
+  // start to the last query's segment end (both rows are non-decreasing).
+  const int* slo = SEG ? p.seg_lo + (int64_t)b * p.N : nullptr;
+  const int* shi = SEG ? p.seg_hi + (int64_t)b * p.N : nullptr;
+  if constexpr (SEG) {
+    k_lo = max(k_lo, clamp_n(slo[wg_q_lo], p.N));
+    k_hi = min(k_hi, clamp_n(shi[wg_q_hi - 1], p.N));
+  }
   const int t_lo = k_lo / BKV;
   // Even tile count (the loop is unrolled by two): an odd range gets one extra tile past
   // the workgroup's keys, which is fully masked (and zero-filled past the sequence end).
+  // An empty range (k_hi <= k_lo, only with segments) gives no tiles at all.
   const int t_hi = t_lo + ((((k_hi + BKV - 1) / BKV) - t_lo + 1) & ~1);
 
   // Keys every query of this wave sees: [all_lo, all_hi).
@@ -103,6 +112,15 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     if (swa) all_lo = q0 + 31 - p.window + 1;
   }
   const int q = q0 + l32;
+  VisRange vis_seg{};  // per-lane visible keys, held only with segments
+  if constexpr (SEG) {
+    if (active) {
+      all_lo = max(all_lo, clamp_n(slo[min(q0 + 31, p.N - 1)], p.N));
+      all_hi = min(all_hi, clamp_n(shi[q0], p.N));
+    }
+    const int qr = min(q, p.N - 1);
+    vis_seg = intersect(keys_of_query(q, p.N, p.causal, p.window), clamp_n(slo[qr], p.N), clamp_n(shi[qr], p.N));
+  }
 
   // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole kernel ----
   i16x8 qf[KT];
@@ -144,6 +162,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   auto step = [&](int t, const char GFA_LDS* kt, const char GFA_LDS* vt, char GFA_LDS* kn,
                   char GFA_LDS* vn) __attribute__((always_inline)) {
     barrier_tile();  // tile t landed; every wave is done reading the other buffers
+    // Issue priority: raised while the wave runs MFMA chains, normal during the softmax, so
+    // that with several waves on a SIMD the matrix unit is fed first and the waves drift
+    // out of phase (one's softmax overlapping another's products): 2-4% at D=256.
+    __builtin_amdgcn_s_setprio(1);
     // The last step re-fetches its own tile into the idle buffers (never read) so the
     // body stays branch-free.
     const int rn = min(t + 1, t_hi - 1) * BKV;
@@ -159,12 +181,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
 #pragma unroll
     for (int sb = 1; sb < SB; ++sb) s[sb] = mma_chain1_lds_b<IS_BF16, KT, 4>(kt, koff0, sb * 32 * (2 * D), qf);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
 
     const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
     if (need_mask) {
       // Rebuilt from the lane id on the (few) boundary tiles rather than held in two
       // registers for the whole kernel.
-      const VisRange vis = keys_of_query(q0 + opaque(l32), p.N, p.causal, p.window);
+      const VisRange vis = SEG ? vis_seg : keys_of_query(q0 + opaque(l32), p.N, p.causal, p.window);
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
@@ -199,10 +222,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
         pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
       }
     }
-    // O^T += V^T P^T with a fixed read-ahead pipeline; the softmax above shares the
-    // scheduling region, so its VALU work can fill the MFMA shadow.
+    // O^T += V^T P^T with a fixed read-ahead pipeline.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
     mma_tr_accumulate_b<IS_BF16, D, DB, BKV / 16, 2, 1>(acc, vt, voff0, pb);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     // One wave per SIMD (D >= 256): keep O^T in AGPRs across iterations (the VGPRs hold Q
     // and the working set). With several waves per SIMD (D <= 128) everything fits the
     // VGPRs; left unpinned, the MFMAs then write VGPRs directly and the softmax needs no
@@ -246,7 +271,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   // ---- epilogue: normalise, store O and LSE ----
   const float l_tot = halves_sum(l_run);
   if (active && q < p.N) {
-    const float inv = 1.0f / l_tot;
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;  // a row that sees no key (empty segment): O = 0
     uint16_t* orow = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh + (int64_t)q * p.ov.sn;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
@@ -266,9 +291,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
 
 // Explicit instantiations of every built variant (both the device code and the host
 // launch stubs must exist for each one).
-#define GFA_FWD_INST(DD, BB, WW, EE)                                              \
-  template __global__ void fwd_kernel<DD, BB, true, WW, EE>(const FwdParams);   \
-  template __global__ void fwd_kernel<DD, BB, false, WW, EE>(const FwdParams);
+#define GFA_FWD_INST(DD, BB, WW, EE)                                                  \
+  template __global__ void fwd_kernel<DD, BB, true, WW, EE, false>(const FwdParams);  \
+  template __global__ void fwd_kernel<DD, BB, false, WW, EE, false>(const FwdParams); \
+  template __global__ void fwd_kernel<DD, BB, true, WW, EE, true>(const FwdParams);   \
+  template __global__ void fwd_kernel<DD, BB, false, WW, EE, true>(const FwdParams);
 GFA_FWD_INST(512, 32, 4, 1)
 GFA_FWD_INST(256, 64, 4, 1)
 GFA_FWD_INST(256, 32, 4, 1)
@@ -281,7 +308,11 @@ GFA_FWD_INST(64, 32, 4, 3)
 
 template <int D, int BKV, bool IS_BF16, int NW, int WPE>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
+  if (p.seg_lo != nullptr) {
+    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, true>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, false>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

@@ -21,7 +21,12 @@ struct QGrid {
   int nblocks;
 };
 
+// Optional segment table, (B, N) int32 each, row b at seg_lo + b * N: token t attends and is
+// attended only within keys [seg_lo[t], seg_hi[t]) (intersected with the causal / window
+// rule). Null when the problem has none (one segment per sequence).
 struct FwdParams {
+  const int* seg_lo;
+  const int* seg_hi;
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
@@ -38,6 +43,8 @@ struct FwdParams {
 };
 
 struct BwdDqParams {
+  const int* seg_lo;  // optional segment table (as FwdParams)
+  const int* seg_hi;
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
@@ -56,6 +63,8 @@ struct BwdDqParams {
 };
 
 struct BwdDkvParams {
+  const int* seg_lo;  // optional segment table (as FwdParams)
+  const int* seg_hi;
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;

@@ -15,13 +15,50 @@ Differences from the reference adapter:
   * the call goes through the registered ``gfa::attn_fwd`` op (``ops.py``), so a model
     under ``torch.compile`` keeps one graph across its attention layers. The op launches on
     its tensors' device itself, which replaces the reference's ``torch.cuda.device`` guard
-    (68-74).
+    (68-74);
+  * padded and packed batches are computed, not ignored (the reference adapter drops
+    ``attention_mask``, 43-47): a padding mask, ``cu_seq_lens_*`` or restarting
+    ``position_ids`` become segment tables (segments.py) for the kernels.
 """
 from __future__ import annotations
 
 import torch
 
+from . import segments as seglib
 from .ops import flash_attn_gqa_op
+
+
+def _segments_for(query, attention_mask, kwargs):
+    """Segment tables for the batch described by the adapter's arguments, or None.
+
+    * ``attention_mask``: the (B, N) padding mask handed over by ``padding_mask_for_engine``
+      (None when nothing is padded); its real tokens must be one run per row;
+    * ``cu_seq_lens_q`` / ``cu_seq_lens_k`` (transformers' packed-sequence keyword
+      arguments): one row of packed sequences;
+    * ``position_ids`` that restart inside a row (packing without a mask, which transformers
+      detects the same way).
+    Anything else the kernels cannot express raises NotImplementedError."""
+    B, _, N, _ = query.shape
+    cu_q, cu_k = kwargs.get("cu_seq_lens_q"), kwargs.get("cu_seq_lens_k")
+    if cu_q is not None or cu_k is not None:
+        if cu_q is None or cu_k is None or not torch.equal(cu_q.to(cu_k.device), cu_k):
+            raise NotImplementedError("packed sequences need equal cu_seq_lens_q and cu_seq_lens_k")
+        if B != 1:
+            raise NotImplementedError("packed sequences (cu_seq_lens) are one row of tokens")
+        return seglib.from_cu_seqlens(cu_q.to(query.device), N)
+    if attention_mask is not None:
+        if attention_mask.dim() != 2:
+            raise NotImplementedError("triton_gqa_attention takes padding masks, not prepared 4-D attention masks")
+        if tuple(attention_mask.shape) != (B, N):
+            raise NotImplementedError(f"padding mask {tuple(attention_mask.shape)} does not match (B, N) = {(B, N)}")
+        try:
+            return seglib.from_padding_mask(attention_mask.to(query.device))
+        except ValueError as e:
+            raise NotImplementedError(str(e)) from None
+    pos = kwargs.get("position_ids")
+    if pos is not None and pos.dim() == 2 and pos.shape[-1] == N and seglib.is_packed(pos):
+        return seglib.from_position_ids(pos.to(query.device).expand(B, N))
+    return None
 
 
 def triton_gqa_attention(module, query, key, value, attention_mask, dropout: float = 0.0,
@@ -31,24 +68,21 @@ def triton_gqa_attention(module, query, key, value, attention_mask, dropout: flo
 
     The kernels build the causal / sliding-window mask from ``module.is_causal`` and
     ``sliding_window`` (reference 30-76). ``attention_mask`` is what the mask creator
-    registered beside this function hands over: None when no token is padded. A padding
-    mask with masked positions, a prepared 4-D mask, or packed sequences (``cu_seq_lens_*``
-    keyword arguments) raise NotImplementedError instead of being ignored, as do softcap
-    and non-zero dropout: never wrong numerics.
+    registered beside this function hands over: None when no token is padded, else the
+    (B, N) padding mask, which becomes a segment table, as do packed sequences
+    (``cu_seq_lens_*`` or restarting ``position_ids``). Padding tokens' output rows are zero
+    (as with transformers' flash-attention path, which drops them). A prepared 4-D mask,
+    softcap and non-zero dropout raise NotImplementedError: never wrong numerics.
     """
     if softcap is not None:
         raise NotImplementedError("triton_gqa_attention does not support softcap")
     if dropout != 0.0:
         raise NotImplementedError("triton_gqa_attention does not support dropout")
-    if attention_mask is not None:
-        if attention_mask.dim() != 2 or not bool(attention_mask.all()):
-            raise NotImplementedError("triton_gqa_attention does not support padding or custom attention masks")
-    if kwargs.get("cu_seq_lens_q") is not None or kwargs.get("cu_seq_lens_k") is not None:
-        raise NotImplementedError("triton_gqa_attention does not support packed sequences (cu_seq_lens)")
+    segments = _segments_for(query, attention_mask, kwargs)
     scale = scaling if scaling is not None else module.head_dim ** -0.5
     slide = int(sliding_window) if sliding_window else 0
     is_causal = getattr(module, "is_causal", True)
-    out = flash_attn_gqa_op(query, key, value, causal=is_causal, slide_size=slide, scale=scale)
+    out = flash_attn_gqa_op(query, key, value, causal=is_causal, slide_size=slide, scale=scale, segments=segments)
     return out.transpose(1, 2).contiguous(), None
 
 

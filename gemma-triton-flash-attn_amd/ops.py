@@ -9,15 +9,24 @@ in the graph: ``flash_attn_gqa_op`` under ``torch.compile(fullgraph=True)`` trac
 without a break, and the captured graph can be replayed with HIP graphs. The kernels and
 numerics are the ones ``flash_attn_gqa_train`` runs.
 
-``attn_fwd(q, k, v, causal, window, scale) -> (O, LSE)``: ``window`` is already normalised
-(0 = none; only honoured when causal), LSE is fp32 (B, Hq, lse_ld(N)) and not
-differentiable. ``attn_bwd(q, k, v, O, LSE, dO, causal, window, scale) -> (dQ, dK, dV)``.
+``attn_fwd(q, k, v, causal, window, scale, seg_lo=None, seg_hi=None) -> (O, LSE)``:
+``window`` is already normalised (0 = none; only honoured when causal), LSE is fp32
+(B, Hq, lse_ld(N)) and not differentiable; ``seg_lo`` / ``seg_hi`` are the optional int32
+(B, N) segment tables of a ragged batch. ``attn_bwd(q, k, v, O, LSE, dO, causal, window,
+scale, seg_lo=None, seg_hi=None) -> (dQ, dK, dV)``.
 """
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 
-from .attention import _backward, _check_inputs, _default_scale, _forward, _layout_ok, _norm_window, _prep, lse_ld
+from .attention import (_backward, _check_inputs, _check_segments, _default_scale, _forward, _layout_ok,
+                        _norm_window, _prep, lse_ld)
+
+
+def _segs(seg_lo, seg_hi):
+    return None if seg_lo is None else (seg_lo, seg_hi)
 
 
 def _out_like(t: torch.Tensor) -> torch.Tensor:
@@ -32,50 +41,56 @@ def _out_like(t: torch.Tensor) -> torch.Tensor:
 
 @torch.library.custom_op("gfa::attn_fwd", mutates_args=(), device_types="cuda")
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, window: int,
-             scale: float) -> tuple[torch.Tensor, torch.Tensor]:
-    o, lse = _forward(q, k, v, causal, window, scale, store_lse=True)
+             scale: float, seg_lo: Optional[torch.Tensor] = None,
+             seg_hi: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    o, lse = _forward(q, k, v, causal, window, scale, store_lse=True, segments=_segs(seg_lo, seg_hi))
     return o, lse
 
 
 @attn_fwd.register_fake
-def _attn_fwd_fake(q, k, v, causal, window, scale):
+def _attn_fwd_fake(q, k, v, causal, window, scale, seg_lo=None, seg_hi=None):
     B, Hq, N, _ = q.shape
     return _out_like(q), q.new_empty((B, Hq, lse_ld(N)), dtype=torch.float32)
 
 
 @torch.library.custom_op("gfa::attn_bwd", mutates_args=(), device_types="cuda")
 def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, lse: torch.Tensor,
-             do: torch.Tensor, causal: bool, window: int, scale: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    dq, dk, dv, _ = _backward(_prep(q), _prep(k), _prep(v), o, lse, do, causal, window, scale)
+             do: torch.Tensor, causal: bool, window: int, scale: float, seg_lo: Optional[torch.Tensor] = None,
+             seg_hi: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    dq, dk, dv, _ = _backward(_prep(q), _prep(k), _prep(v), o, lse, do, causal, window, scale,
+                              segments=_segs(seg_lo, seg_hi))
     return dq, dk, dv
 
 
 @attn_bwd.register_fake
-def _attn_bwd_fake(q, k, v, o, lse, do, causal, window, scale):
+def _attn_bwd_fake(q, k, v, o, lse, do, causal, window, scale, seg_lo=None, seg_hi=None):
     return _out_like(q), _out_like(k), _out_like(v)
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, causal, window, scale = inputs
+    q, k, v, causal, window, scale, seg_lo, seg_hi = inputs
     o, lse = output
-    ctx.save_for_backward(q, k, v, o, lse)
+    ctx.save_for_backward(q, k, v, o, lse, seg_lo, seg_hi)
     ctx.causal, ctx.window, ctx.scale = causal, window, scale
     ctx.mark_non_differentiable(lse)
 
 
 def _attn_fwd_backward(ctx, do, _dlse):
-    q, k, v, o, lse = ctx.saved_tensors
-    dq, dk, dv = attn_bwd(q, k, v, o, lse, do, ctx.causal, ctx.window, ctx.scale)
-    return dq, dk, dv, None, None, None
+    q, k, v, o, lse, seg_lo, seg_hi = ctx.saved_tensors
+    dq, dk, dv = attn_bwd(q, k, v, o, lse, do, ctx.causal, ctx.window, ctx.scale, seg_lo, seg_hi)
+    return dq, dk, dv, None, None, None, None, None
 
 
 attn_fwd.register_autograd(_attn_fwd_backward, setup_context=_setup_context)
 
 
-def flash_attn_gqa_op(q, k, v, causal=False, slide_size=0, *, scale=None):
+def flash_attn_gqa_op(q, k, v, causal=False, slide_size=0, *, scale=None, segments=None):
     """``flash_attn_gqa_train`` through the registered op: same arguments, kernels and
     results, and traceable by ``torch.compile`` (no graph break at the attention call)."""
     _check_inputs(q, k, v)
+    segments = _check_segments(segments, q)
     window = _norm_window(causal, slide_size, q.shape[2])
-    o, _ = torch.ops.gfa.attn_fwd(q, k, v, bool(causal), int(window), _default_scale(q.shape[3], scale))
+    seg_lo, seg_hi = segments if segments is not None else (None, None)
+    o, _ = torch.ops.gfa.attn_fwd(q, k, v, bool(causal), int(window), _default_scale(q.shape[3], scale),
+                                  seg_lo, seg_hi)
     return o

@@ -12,7 +12,18 @@
  * tiles of up to 64 rows, so rows N..lse_ld-1 must exist (their values are never used).
  * Query head h reads KV head h / (Hq / Hkv) (contiguous groups). head_dim is 64, 128, 256
  * or 512 (the reference documents 64-512, powers of two); anything else returns
- * GFA_ERR_UNSUPPORTED, as does a (batch, head) slice spanning more than 4 GiB.
+ * GFA_ERR_UNSUPPORTED, as does a (batch, head) slice that, with 127 rows of margin past its
+ * end, spans more than 4 GiB.
+ *
+ * Variable-length and padded batches: seg_lo / seg_hi (optional, both or neither) are
+ * int32 (B, N) tables, row b at seg_lo + b * N. Token t of row b attends, and is attended
+ * by, only the tokens of keys [seg_lo[t], seg_hi[t]), intersected with the causal / window
+ * rule. Each row must partition [0, N) into consecutive runs: a segment, whose tokens all
+ * carry lo = first token and hi = one past its last, or padding, where token t carries
+ * lo = hi = t (an empty segment: its O row is 0, its LSE -inf, and its dQ/dK/dV rows 0).
+ * So both columns are non-decreasing. Left and right padding and packed sequences (the
+ * reference's unsupported varlen case, README.md:255-262) are all such tables. The kernels
+ * clamp table values to [0, N], so no content makes them address outside the tensors.
  *
  * The entry points replace the reference's Triton launch sites (file:line in
  * /root/reference, zzhhjjj/gemma-triton-flash-attn):
@@ -37,7 +48,7 @@
 extern "C" {
 #endif
 
-#define GFA_VERSION 101 /* 1.0.1: LSE rows padded to 64 */
+#define GFA_VERSION 102 /* 1.0.2: optional segment tables (variable-length / padded batches) */
 
 typedef enum {
   GFA_DTYPE_FP16 = 0,
@@ -79,6 +90,8 @@ typedef struct {
   int32_t block_kv;    /* 0 = registry default, else a built tile width */
   int32_t lse_ld;      /* row length of lse (>= GFA_LSE_LD(seq_len)); ignored when lse == NULL */
   void* stream;        /* hipStream_t */
+  const int32_t* seg_lo; /* optional (B, N) segment table (see above); NULL = one segment per row */
+  const int32_t* seg_hi;
 } gfa_fwd_args;
 
 typedef struct {
@@ -104,6 +117,8 @@ typedef struct {
   void* workspace;        /* >= gfa_bwd_workspace_size(...) bytes when q_splits > 1 */
   size_t workspace_bytes;
   void* stream;
+  const int32_t* seg_lo;  /* the forward's segment table, or NULL */
+  const int32_t* seg_hi;
 } gfa_bwd_args;
 
 /* Tile configuration the library uses for one problem (mirrors the Python registry). */

@@ -15,6 +15,15 @@ What it restates (all paths under /root/reference, zzhhjjj/gemma-triton-flash-at
     dS = P * (dP - delta), dQ = scale * dS K), 1192-1202 (dV = P^T dO, dK = scale * dS^T Q,
     summed over the query heads of a KV group).
 
+Variable-length / padded batches (the build's segment tables, include/gfa.h; the reference
+lists varlen and padding masks as unsupported, README.md:255-262, and its HF adapter ignores
+the mask, hf_integration.py:43-47): ``segments = (lo, hi)``, two (B, N) integer arrays; key
+j is visible to query i of row b only if lo[b, i] <= j < hi[b, i], on top of the causal /
+window rule. A query row with no visible key has O = 0 and LSE = -inf, and contributes no
+gradient. Pinned by tests/test_oracle.py against torch SDPA with the equivalent boolean
+mask (rows with a visible key) and against the segment-free oracle run on every segment
+alone (padded and packed batches).
+
 Two implementations of the same equations:
   * ``forward`` / ``backward``: numpy float64, dense (N x N per head) - small cases and
     golden vectors;
@@ -47,49 +56,62 @@ def allowed_mask(n: int, causal: bool, window: int = 0) -> np.ndarray:
     return m
 
 
+def _row_mask(mask, segments, b):
+    """Allowed-mask of batch row b: the causal / window mask restricted to segments."""
+    if segments is None:
+        return mask
+    lo = np.asarray(segments[0])[b][:, None]
+    hi = np.asarray(segments[1])[b][:, None]
+    j = np.arange(mask.shape[1])[None, :]
+    return mask & (j >= lo) & (j < hi)
+
+
 def _default_scale(d: int, scale):
     return 1.0 / math.sqrt(d) if scale is None else float(scale)
 
 
-def forward(q, k, v, causal=False, window=0, scale=None):
+def forward(q, k, v, causal=False, window=0, scale=None, segments=None):
     """O (B, Hq, N, D) and natural-log LSE (B, Hq, N), float64."""
     q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     sc = _default_scale(D, scale)
-    mask = allowed_mask(N, causal, window)
+    base = allowed_mask(N, causal, window)
     o = np.empty_like(q)
     lse = np.empty((B, Hq, N))
     for b in range(B):
+        mask = _row_mask(base, segments, b)
+        seen = mask.any(axis=1)[:, None]
         for h in range(Hq):
             g = h * Hkv // Hq
             s = sc * (q[b, h] @ k[b, g].T)
             s = np.where(mask, s, -np.inf)
-            mx = s.max(axis=1, keepdims=True)
-            p = np.exp(s - mx)
+            mx = np.where(seen, s.max(axis=1, keepdims=True), 0.0)
+            p = np.where(mask, np.exp(s - mx), 0.0)
             l = p.sum(axis=1, keepdims=True)
-            o[b, h] = (p / l) @ v[b, g]
-            lse[b, h] = (mx + np.log(l))[:, 0]
+            o[b, h] = np.where(seen, p / np.where(seen, l, 1.0), 0.0) @ v[b, g]
+            lse[b, h] = np.where(seen, mx + np.log(np.where(seen, l, 1.0)), -np.inf)[:, 0]
     return o, lse
 
 
-def backward(q, k, v, do, causal=False, window=0, scale=None):
+def backward(q, k, v, do, causal=False, window=0, scale=None, segments=None):
     """dQ, dK, dV (float64) and delta = rowsum(dO * O) for the loss sum(O * dO)."""
     q, k, v, do = (np.asarray(x, dtype=np.float64) for x in (q, k, v, do))
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     sc = _default_scale(D, scale)
-    o, lse = forward(q, k, v, causal, window, scale)
-    mask = allowed_mask(N, causal, window)
+    o, lse = forward(q, k, v, causal, window, scale, segments)
+    base = allowed_mask(N, causal, window)
     dq = np.zeros_like(q)
     dk = np.zeros_like(k)
     dv = np.zeros_like(v)
     delta = (do * o).sum(axis=-1)
     for b in range(B):
+        mask = _row_mask(base, segments, b)
         for h in range(Hq):
             g = h * Hkv // Hq
             s = sc * (q[b, h] @ k[b, g].T)
-            p = np.where(mask, np.exp(s - lse[b, h][:, None]), 0.0)
+            p = np.where(mask, np.exp(np.where(mask, s - lse[b, h][:, None], 0.0)), 0.0)
             dp = do[b, h] @ v[b, g].T
             ds = p * (dp - delta[b, h][:, None])
             dq[b, h] = sc * (ds @ k[b, g])
@@ -102,7 +124,7 @@ def backward(q, k, v, do, causal=False, window=0, scale=None):
 # torch float32, query-chunked: the same equations for shapes too large for dense N x N.
 # ----------------------------------------------------------------------------------------
 
-def _chunk_mask(torch, q_lo, q_hi, n, causal, window, device):
+def _chunk_mask(torch, q_lo, q_hi, n, causal, window, device, segments=None, b=0):
     i = torch.arange(q_lo, q_hi, device=device)[:, None]
     j = torch.arange(n, device=device)[None, :]
     m = torch.ones((q_hi - q_lo, n), dtype=torch.bool, device=device)
@@ -110,11 +132,16 @@ def _chunk_mask(torch, q_lo, q_hi, n, causal, window, device):
         m &= j <= i
         if window and 0 < window < n:
             m &= (i - j) < window
+    if segments is not None:
+        lo = segments[0][b, q_lo:q_hi].to(device)[:, None]
+        hi = segments[1][b, q_lo:q_hi].to(device)[:, None]
+        m &= (j >= lo) & (j < hi)
     return m
 
 
-def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024):
-    """torch fp32 O and LSE for (B, H, N, D) tensors of any float dtype / device."""
+def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024, segments=None):
+    """torch fp32 O and LSE for (B, H, N, D) tensors of any float dtype / device.
+    ``segments``: (lo, hi) integer tensors (B, N), as in ``forward``."""
     import torch
 
     B, Hq, N, D = q.shape
@@ -132,16 +159,20 @@ def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024):
                 for lo in range(0, N, chunk):
                     hi = min(N, lo + chunk)
                     s = (qf[lo:hi] @ kt) * sc
-                    s = s.masked_fill(~_chunk_mask(torch, lo, hi, N, causal, window, q.device), float("-inf"))
-                    m = s.amax(dim=1, keepdim=True)
+                    mask = _chunk_mask(torch, lo, hi, N, causal, window, q.device, segments, b)
+                    seen = mask.any(dim=1, keepdim=True)
+                    s = s.masked_fill(~mask, float("-inf"))
+                    m = torch.where(seen, s.amax(dim=1, keepdim=True), torch.zeros_like(s[:, :1]))
                     p = torch.exp(s - m)
                     l = p.sum(dim=1, keepdim=True)
-                    o[b, h, lo:hi] = (p @ vf) / l
-                    lse[b, h, lo:hi] = (m + torch.log(l))[:, 0]
+                    l1 = torch.where(seen, l, torch.ones_like(l))
+                    o[b, h, lo:hi] = torch.where(seen, (p @ vf) / l1, torch.zeros_like(qf[lo:hi]))
+                    lse[b, h, lo:hi] = torch.where(seen, m + torch.log(l1), torch.full_like(l, float("-inf")))[:, 0]
     return o, lse
 
 
-def backward_chunked(q, k, v, do, causal=False, window=0, scale=None, chunk=1024, o=None, lse=None):
+def backward_chunked(q, k, v, do, causal=False, window=0, scale=None, chunk=1024, o=None, lse=None,
+                     segments=None):
     """torch fp32 dQ, dK, dV, delta. ``o``/``lse`` may be passed to skip the recomputation."""
     import torch
 
@@ -149,7 +180,7 @@ def backward_chunked(q, k, v, do, causal=False, window=0, scale=None, chunk=1024
     Hkv = k.shape[1]
     sc = _default_scale(D, scale)
     if o is None or lse is None:
-        o, lse = forward_chunked(q, k, v, causal, window, scale, chunk)
+        o, lse = forward_chunked(q, k, v, causal, window, scale, chunk, segments)
     dq = torch.empty((B, Hq, N, D), dtype=torch.float32, device=q.device)
     dk = torch.zeros((B, Hkv, N, D), dtype=torch.float32, device=q.device)
     dv = torch.zeros((B, Hkv, N, D), dtype=torch.float32, device=q.device)
@@ -165,9 +196,9 @@ def backward_chunked(q, k, v, do, causal=False, window=0, scale=None, chunk=1024
                 dof = do[b, h].float()
                 for lo in range(0, N, chunk):
                     hi = min(N, lo + chunk)
-                    mask = _chunk_mask(torch, lo, hi, N, causal, window, q.device)
+                    mask = _chunk_mask(torch, lo, hi, N, causal, window, q.device, segments, b)
                     s = (qf[lo:hi] @ kt) * sc
-                    p = torch.exp(s - lse[b, h, lo:hi, None].float()).masked_fill(~mask, 0.0)
+                    p = torch.exp((s - lse[b, h, lo:hi, None].float()).masked_fill(~mask, 0.0)).masked_fill(~mask, 0.0)
                     dp = dof[lo:hi] @ vt
                     ds = p * (dp - delta[b, h, lo:hi, None])
                     dq[b, h, lo:hi] = (ds @ kf) * sc

@@ -47,16 +47,17 @@ def test_oracle_attention_matches_sdpa_inside_the_model():
     assert float((a - b).abs().max()) < 1e-3
 
 
-def test_padding_mask_reaches_the_adapter_and_is_refused():
+def test_padding_mask_reaches_the_adapter_and_becomes_segments():
     """transformers drops a 2-D padding mask for attention functions without a mask creator.
     register_triton_attention installs one, so a padded batch hands the adapter its padding
-    mask (and an unpadded one hands over None); the adapter refuses masked positions instead
-    of ignoring them."""
+    mask (and an unpadded one hands over None); the adapter turns it, packed cu_seq_lens and
+    restarting position ids into segment tables, and refuses what a table cannot express."""
     from types import SimpleNamespace
 
     from transformers import AttentionInterface
 
     import gemma_triton_flash_attn_amd as gfa
+    from gemma_triton_flash_attn_amd.hf_integration import _segments_for
 
     seen = []
 
@@ -86,9 +87,23 @@ def test_padding_mask_reaches_the_adapter_and_is_refused():
         model(input_ids=ids, attention_mask=torch.ones(2, 24, dtype=torch.long), use_cache=False)
     assert seen == [None, None]
 
-    mod = SimpleNamespace(head_dim=256, is_causal=True)
     q = torch.zeros(2, 2, 24, 256)
-    with pytest.raises(NotImplementedError, match="padding"):
-        gfa.triton_gqa_attention(mod, q, q, q, pad.bool())
-    with pytest.raises(NotImplementedError, match="packed"):
-        gfa.triton_gqa_attention(mod, q, q, q, None, cu_seq_lens_q=torch.tensor([0, 10, 24]))
+    lo, hi = _segments_for(q, pad.bool(), {})
+    assert lo[1].tolist() == [0] * 18 + list(range(18, 24)) and hi[1].tolist() == [18] * 18 + list(range(18, 24))
+    assert lo[0].tolist() == [0] * 24 and hi[0].tolist() == [24] * 24
+    assert _segments_for(q, None, {"position_ids": torch.arange(24)[None]}) is None
+    q1 = q[:1]
+    lo, hi = _segments_for(q1, None, {"cu_seq_lens_q": torch.tensor([0, 10, 24]), "cu_seq_lens_k": torch.tensor([0, 10, 24])})
+    assert lo.tolist() == [[0] * 10 + [10] * 14] and hi.tolist() == [[10] * 10 + [24] * 14]
+    pos = torch.cat([torch.arange(10), torch.arange(14)])[None]
+    plo, phi = _segments_for(q1, None, {"position_ids": pos})
+    assert torch.equal(plo, lo) and torch.equal(phi, hi)
+    mod = SimpleNamespace(head_dim=256, is_causal=True)
+    with pytest.raises(NotImplementedError, match="4-D"):
+        gfa.triton_gqa_attention(mod, q, q, q, torch.ones(2, 1, 24, 24, dtype=torch.bool))
+    holes = torch.ones(2, 24, dtype=torch.bool)
+    holes[0, 5] = False
+    with pytest.raises(NotImplementedError, match="contiguous"):
+        gfa.triton_gqa_attention(mod, q, q, q, holes)
+    with pytest.raises(NotImplementedError, match="cu_seq_lens"):
+        gfa.triton_gqa_attention(mod, q1, q1, q1, None, cu_seq_lens_q=torch.tensor([0, 10, 24]))
