@@ -141,22 +141,56 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
 #pragma unroll
     for (int j = 0; j < DB; ++j) acc[i][j] = f32x16{};
 
+  // Per-lane LDS offsets of the tile reads. At D=128 (two waves per SIMD, register-bound)
+  // one base each: kstep_off and mma_tr_accumulate_b derive the others with an XOR next to
+  // each read, where eight-entry offset tables would cost 14 registers (5% faster measured).
+  // The other head dims keep the tables (measured 2-4% faster there).
+  constexpr bool ONE_BASE = D == 128;
+  const int roff0 = l32 * (2 * D) + ((h ^ swz<D>(l32)) << 4);  // tile row l32, chunk h (k-step 0)
   int roff[8];  // tile rows (A operand of S / dP): row l32, chunk 2*kk + h  (+256 * (kk >> 3))
 #pragma unroll
   for (int kl = 0; kl < 8; ++kl) roff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4);
-  int toffA[4], toffB[4];  // tiles read transposed (A operands of dV^T, dK^T)
+  int toff0;  // tiles read transposed (A operands of dV^T, dK^T): rows 4h + t/4, column block 0
+  int toffA[4], toffB[4];
   {
     const int t16 = lane & 15;
     const int half16 = (lane >> 4) & 1;
     const int rA = 4 * h + (t16 >> 2);
     const int rB = rA + 8;
+    const int c0 = 2 * half16 + ((t16 >> 1) & 1);
+    toff0 = rA * (2 * D) + ((c0 ^ swz<D>(rA)) << 4) + (t16 & 1) * 8;
 #pragma unroll
     for (int dl = 0; dl < 4; ++dl) {
-      const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
+      const int c = 4 * dl + c0;
       toffA[dl] = rA * (2 * D) + ((c ^ swz<D>(rA)) << 4) + (t16 & 1) * 8;
       toffB[dl] = rB * (2 * D) + ((c ^ swz<D>(rB)) << 4) + (t16 & 1) * 8;
     }
   }
+  // Score chains (the first one of a step with NL tile-copy instructions spread over it) and
+  // accumulations from tiles read transposed, in the offset form chosen above.
+  auto chain = [&](const char GFA_LDS* tile, int extra, const i16x8 (&bf)[KT]) __attribute__((always_inline)) {
+    if constexpr (ONE_BASE) {
+      return mma_chain1_lds_b<IS_BF16, KT, 4, 1>(tile, roff0, extra, bf);
+    } else {
+      return mma_chain1_lds<IS_BF16, KT, 4, 1>(tile, roff, extra, bf);
+    }
+  };
+  auto chain_ld = [&](auto nl, const char GFA_LDS* tile, const i16x8 (&bf)[KT], auto&& ld) __attribute__((always_inline)) {
+    constexpr int NL = decltype(nl)::value;
+    if constexpr (ONE_BASE) {
+      return mma_chain1_lds_ld_b<IS_BF16, KT, 4, NL>(tile, roff0, 0, bf, ld);
+    } else {
+      return mma_chain1_lds_ld<IS_BF16, KT, 4, NL>(tile, roff, 0, bf, ld);
+    }
+  };
+  auto accumulate = [&](f32x16 (&acc_)[DB], const char GFA_LDS* tile, const i16x8 (&bop)[BQ / 16])
+                        __attribute__((always_inline)) {
+    if constexpr (ONE_BASE) {
+      mma_tr_accumulate_b<IS_BF16, D, DB, BQ / 16, 4, 1>(acc_, tile, toff0, bop);
+    } else {
+      mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 4, 1>(acc_, tile, toffA, toffB, bop);
+    }
+  };
 
   TileLoader<D, BQ, NW> qload, dload;
   qload.init(p.q, p.qv.sn, p.N, wave, lane);
@@ -242,7 +276,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
         if (sb == 0) {
-          s[sb] = mma_chain1_lds_ld<IS_BF16, KT, 4, 2 * NI>(ct, roff, 0, sf[0], [&](int i) {
+          s[sb] = chain_ld(std::integral_constant<int, 2 * NI>{}, ct, sf[0], [&](int i) {
             if (i < NI) {
               qload.load_part(i, row_n, qn);
             } else {
@@ -250,7 +284,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
             }
           });
         } else {
-          s[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(ct, roff, sb * 32 * (2 * D), sf[0]);
+          s[sb] = chain(ct, sb * 32 * (2 * D), sf[0]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -278,7 +312,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       i16x8 pb[BQ / 16];
       pack(s, pb);
       __builtin_amdgcn_sched_barrier(0);
-      mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 4, 1>(acc[0], tt, toffA, toffB, pb);
+      accumulate(acc[0], tt, pb);
       __builtin_amdgcn_sched_barrier(0);
     } else {
       // S = Q K^T, dP = dO V^T, then dV^T += dO^T P and dK^T += Q^T dS.
@@ -287,18 +321,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
         if (sb == 0) {
-          s[sb] = mma_chain1_lds_ld<IS_BF16, KT, 4, NI>(qt, roff, 0, sf[0], [&](int i) { qload.load_part(i, row_n, qn); });
+          s[sb] = chain_ld(std::integral_constant<int, NI>{}, qt, sf[0], [&](int i) { qload.load_part(i, row_n, qn); });
         } else {
-          s[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(qt, roff, sb * 32 * (2 * D), sf[0]);
+          s[sb] = chain(qt, sb * 32 * (2 * D), sf[0]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
         if (sb == 0) {
-          dp[sb] = mma_chain1_lds_ld<IS_BF16, KT, 4, NI>(dt, roff, 0, sf[1], [&](int i) { dload.load_part(i, row_n, dn); });
+          dp[sb] = chain_ld(std::integral_constant<int, NI>{}, dt, sf[1], [&](int i) { dload.load_part(i, row_n, dn); });
         } else {
-          dp[sb] = mma_chain1_lds<IS_BF16, KT, 4, 1>(dt, roff, sb * 32 * (2 * D), sf[1]);
+          dp[sb] = chain(dt, sb * 32 * (2 * D), sf[1]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -314,9 +348,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       pack(s, pb);
       pack(dp, dsb);
       __builtin_amdgcn_sched_barrier(0);
-      mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 4, 1>(acc[0], dt, toffA, toffB, pb);
+      accumulate(acc[0], dt, pb);
       __builtin_amdgcn_sched_barrier(0);
-      mma_tr_accumulate<IS_BF16, D, DB, BQ / 16, 4, 1>(acc[NS - 1], qt, toffA, toffB, dsb);
+      accumulate(acc[NS - 1], qt, dsb);
       __builtin_amdgcn_sched_barrier(0);
     }
     // D >= 256: the accumulators fill the AGPRs and stay there. At D=64 everything fits the
