@@ -236,15 +236,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       }
     }
   };
-  // dS = P * (dP - delta) in place of dP; P == 0 (masked or underflowed) gives exactly 0,
-  // also for padding rows whose delta is not defined.
+  // dS = P * (dP - delta) in place of dP. Masked entries have P = 0 and give 0: delta is
+  // finite on every row a tile covers (the dQ kernel writes the rows past N of the last
+  // 32-row block too), so no guard is needed.
   auto make_ds = [&](f32x16& dp, const f32x4 pv4[4], const f32x4 (&del)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = 4 * j + e;
-        dp[r] = pv4[j][e] != 0.f ? pv4[j][e] * (dp[r] - del[j][e]) : 0.f;
+        dp[r] = pv4[j][e] * (dp[r] - del[j][e]);
       }
     }
   };

@@ -138,7 +138,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     barrier_lds();
     delta += *reinterpret_cast<const float GFA_LDS*>(xch + (wave ^ 1) * XCH + lane * 4);
   }
-  if (active && q < p.N && dh == 0 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.lse_ld + q] = delta;
+  // Written for every row of an active block, also the rows past N in the last one (they
+  // repeat row N-1's value): the dK/dV kernel reads whole 32-row tiles of delta and relies
+  // on them being finite (its dS = P (dP - delta) with P = 0 on those rows).
+  if (active && dh == 0 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.lse_ld + q] = delta;
   const float lse_log2 = p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + qrow] * kLog2e;
 
   f32x16 acc[DBH];

@@ -101,7 +101,9 @@ typedef struct {
   const void* o;
   const void* dout;
   const float* lse; /* from gfa_fwd, (B, Hq, lse_ld) */
-  float* delta;     /* (B, Hq, lse_ld) scratch written by the dQ kernel: rowsum(dO * O) */
+  float* delta;     /* (B, Hq, lse_ld) scratch written by the dQ kernel: rowsum(dO * O), for
+                       every row below seq_len rounded up to 32 (rows past seq_len repeat
+                       row seq_len-1) */
   void* dq;
   void* dk;
   void* dv;

@@ -216,3 +216,35 @@ def test_block_kv_override(block_kv, D, device):
     o_ref, _ = orc.forward(_np(q), _np(k), _np(v), True, 50)
     assert float(np.abs(_np(o) - o_ref).max()) <= O_TOL[torch.bfloat16]
     assert float((o.float() - o_def.float()).abs().max()) <= 1e-2
+
+
+@pytest.mark.parametrize("N,D,window,segs", [(100, 256, 0, False), (77, 64, 16, False), (130, 128, 0, False),
+                                             (45, 512, 0, False), (150, 256, 48, True)])
+def test_delta_scratch_garbage_does_not_leak(N, D, window, segs, device):
+    """The dK/dV kernel reads whole 32-row tiles of delta and multiplies masked entries
+    (P = 0) by (dP - delta) without a guard: the dQ kernel must write every delta row such
+    a tile covers, also those past N. A delta buffer prefilled with NaN (and a DKV-only call
+    reading it after a DQ call) must give the same gradients as a fresh buffer, bit for bit."""
+    from gemma_triton_flash_attn_amd import _lib
+    from gemma_triton_flash_attn_amd.attention import _backward, _forward, lse_ld
+
+    B, Hq, Hkv = 2, 4, 2
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, torch.bfloat16, device, seed=N + D)
+    segments = None
+    if segs:
+        import gemma_triton_flash_attn_amd as gfa
+        segments = gfa.segments.from_lengths([N - 17, N // 2], N, device=device)
+    sc = D ** -0.5
+    o, lse = _forward(q, k, v, True, window, sc, store_lse=True, segments=segments)
+    ref = _backward(q, k, v, o, lse, do, True, window, sc, segments=segments)
+    bufs = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+            torch.full((B, Hq, lse_ld(N)), float("nan"), dtype=torch.float32, device=device))
+    _backward(q, k, v, o, lse, do, True, window, sc, stages=_lib.GFA_BWD_DQ, out=bufs, segments=segments)
+    _backward(q, k, v, o, lse, do, True, window, sc, stages=_lib.GFA_BWD_DKV, out=bufs, segments=segments)
+    torch.cuda.synchronize()
+    for a, r in zip(bufs[:3], ref[:3]):
+        assert torch.isfinite(a.float()).all()
+        assert torch.equal(a, r)
+    # every delta row a 32-row tile covers is finite
+    n32 = (N + 31) // 32 * 32
+    assert torch.isfinite(bufs[3][:, :, :n32]).all()
