@@ -143,6 +143,18 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   // on them being finite (its dS = P (dP - delta) with P = 0 on those rows).
   if (active && dh == 0 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.lse_ld + q] = delta;
   const float lse_log2 = p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + qrow] * kLog2e;
+  // D >= 256: the dP^T chain starts from -delta (lane = query), so it yields dP - delta
+  // directly and dS = P (dP - delta) costs one multiply (16 AGPRs, which the one-wave-per-SIMD
+  // budget has; at D <= 128 they would cost an occupancy step, so the subtraction stays).
+  // With the head dim split over a pair, only the first half starts there (the partials are
+  // summed).
+  constexpr bool DP_FROM_DELTA = D >= 256;
+  f32x16 neg_delta = f32x16{};
+  if constexpr (DP_FROM_DELTA) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) neg_delta[r] = dh == 0 ? -delta : 0.f;
+  }
+  const float delta_left = DP_FROM_DELTA ? 0.f : delta;  // what dS still subtracts
 
   f32x16 acc[DBH];
 #pragma unroll
@@ -192,12 +204,13 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     f32x16 s[SB], dp[SB];
     s[0] = mma_chain1_lds_ld<IS_BF16, KTH, 4, NI>(kt, koff, 0, qf, [&](int i) { kload.load_part(i, rn, kn); });
     __builtin_amdgcn_sched_barrier(0);
-    dp[0] = mma_chain1_lds_ld<IS_BF16, KTH, 4, NI>(vt, koff, 0, df, [&](int i) { vload.load_part(i, rn, vn); });
+    dp[0] = mma_chain1_lds_ld<IS_BF16, KTH, 4, NI>(vt, koff, 0, df, [&](int i) { vload.load_part(i, rn, vn); },
+                                                   neg_delta);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int sb = 1; sb < SB; ++sb) {
       s[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
-      dp[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(vt, koff, sb * 32 * (2 * D), df);
+      dp[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(vt, koff, sb * 32 * (2 * D), df) + neg_delta;
     }
     if constexpr (SPLIT == 2) {
 #pragma unroll
@@ -230,7 +243,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[sb][r] = fast_exp2(s[sb][r] * p.scale_log2 - lse_log2) * (dp[sb][r] - delta);
+      for (int r = 0; r < 16; ++r) {
+        const float dpd = DP_FROM_DELTA ? dp[sb][r] : dp[sb][r] - delta_left;
+        s[sb][r] = fast_exp2(s[sb][r] * p.scale_log2 - lse_log2) * dpd;
+      }
     }
     if (need_mask) {
 #pragma unroll

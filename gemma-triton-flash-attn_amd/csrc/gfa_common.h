@@ -342,12 +342,13 @@ __device__ __forceinline__ f32x16 mma_chain1_lds_ld_b(const char GFA_LDS* tile, 
 // every KT / NL MFMAs. A wave issues in order and the copies of all its workgroup's waves
 // share the CU's texture path (each copy instruction moves 1 KB), so a run of copy issues
 // holds up the MFMAs behind it; one copy every few MFMAs keeps the MFMA stream moving.
+// c_init: the accumulator the chain starts from (zero by default).
 template <bool IS_BF16, int KT, int PF, int NL, typename LD>
 __device__ __forceinline__ f32x16 mma_chain1_lds_ld(const char GFA_LDS* tile, const int (&koff)[8], int extra,
-                                                    const i16x8 (&bf)[KT], LD&& ld) {
+                                                    const i16x8 (&bf)[KT], LD&& ld, const f32x16& c_init = f32x16{}) {
   static_assert(PF <= KT && NL >= 1 && KT % NL == 0, "bad chain shape");
   constexpr int EV = KT / NL;
-  f32x16 c = f32x16{};
+  f32x16 c = c_init;
   i16x8 a[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, koff[i & 7] + 256 * (i >> 3) + extra);
