@@ -202,7 +202,8 @@ int gfa_fwd(const gfa_fwd_args* a) {
     for (int i = 0; i < 4; ++i)
       if ((rc = check_span(names[i], *views[i], a->seq_len, a->head_dim))) return rc;
   }
-  if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
+  if (!std::isfinite(a->scale) || !(a->scale > 0.f))
+    return fail(GFA_ERR_INVALID_ARGUMENT, "scale=%g must be finite and positive", (double)a->scale);
   if ((rc = check_segments(a->seg_lo, a->seg_hi))) return rc;
   const Entry* e = lookup(a->head_dim);
   const bool windowed = a->causal && a->window > 0 && a->window < a->seq_len;
@@ -284,7 +285,8 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   if (a->lse_ld < GFA_LSE_LD(a->seq_len) || (a->lse_ld & 3) || !aligned16(a->lse) || !aligned16(delta_buf))
     return fail(GFA_ERR_INVALID_ARGUMENT, "lse_ld=%d must be >= %d (multiple of 4, 16-byte aligned lse/delta)",
                 a->lse_ld, GFA_LSE_LD(a->seq_len));
-  if (!std::isfinite(a->scale)) return fail(GFA_ERR_INVALID_ARGUMENT, "scale is not finite");
+  if (!std::isfinite(a->scale) || !(a->scale > 0.f))
+    return fail(GFA_ERR_INVALID_ARGUMENT, "scale=%g must be finite and positive", (double)a->scale);
   if ((rc = check_segments(a->seg_lo, a->seg_hi))) return rc;
   const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
   if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);

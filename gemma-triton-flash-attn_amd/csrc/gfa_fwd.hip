@@ -198,16 +198,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
         }
       }
     }
+    // Row max of the scaled scores as scale * (max of the raw ones): the scale is positive
+    // (checked at the boundary; masking to -inf before scaling needs that too), so one
+    // multiply replaces sixteen. The exponent argument scales each score in its FMA.
     float mt = -INFINITY;
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[sb][r] *= p.scale_log2;
-        mt = fmaxf(mt, s[sb][r]);
-      }
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sb][r]);
     }
-    mt = halves_max(mt);
+    mt = halves_max(mt) * p.scale_log2;
     // First tile with a visible key fixes m_ref; acc and l are still zero for this row.
     m_ref = (m_ref == kNegBig && mt > kNegBig) ? mt : m_ref;
     ovf = ovf || (mt > m_ref + kMargin);
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = fast_exp2(s[sb][r] - m_ref);
+        const float pv = fast_exp2(s[sb][r] * p.scale_log2 - m_ref);
         l_run += pv;
         pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
       }

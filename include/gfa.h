@@ -85,7 +85,7 @@ typedef struct {
   int32_t batch, heads_q, heads_kv, seq_len, head_dim;
   int32_t causal;      /* 0 / 1 */
   int32_t window;      /* sliding window; 0 = off; honoured only when causal; >= seq_len -> off */
-  float scale;         /* softmax scale; the reference uses 1/sqrt(head_dim) */
+  float scale;         /* softmax scale, finite and > 0; the reference uses 1/sqrt(head_dim) */
   int32_t dtype;       /* gfa_dtype, shared by q/k/v/o */
   int32_t block_kv;    /* 0 = registry default, else a built tile width */
   int32_t lse_ld;      /* row length of lse (>= GFA_LSE_LD(seq_len)); ignored when lse == NULL */

@@ -97,6 +97,8 @@ def _fwd_args(**over):
     (dict(q=260), 1),                     # misaligned pointer
     (dict(lse_ld=16), 1),                 # lse rows shorter than GFA_LSE_LD(N)
     (dict(scale=float("nan")), 1),
+    (dict(scale=0.0), 1),                 # the kernels mask with -inf before scaling: scale > 0
+    (dict(scale=-0.125), 1),
     (dict(block_kv=48), 2),               # no such forward tile
     (dict(k_strides=_lib.Strides(8, 8, 4)), 1),  # row stride not a multiple of 8 elements
 ])
@@ -134,6 +136,10 @@ def test_bwd_rejects_bad_arguments():
     assert need == 4 * 2 * 1 * 1 * 64 * 512 * 4
     a.workspace, a.workspace_bytes = 4096, need - 1
     assert lib.gfa_bwd(ctypes.byref(a)) == 3
+    a.workspace, a.workspace_bytes = 4096, need
+    for bad in (0.0, -0.5, float("inf")):
+        a.scale = bad
+        assert lib.gfa_bwd(ctypes.byref(a)) == 1
 
 
 def test_python_api_validation_needs_no_gpu():
