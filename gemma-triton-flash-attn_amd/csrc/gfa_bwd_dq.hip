@@ -7,14 +7,15 @@
 //   dS_ij   = P_ij * (dO_i.v_j - delta_i)                 (masked -> 0, cast to input dtype)
 //   dQ_i    = s * sum_j dS_ij k_j
 //
-// MI355X design: a wave pair owns 32 query rows of one head; each wave keeps its
-// head-dim half of Q and dO in VGPRs (B operands of S^T = K Q^T and dP^T = V dO^T,
-// lane = query), computes partial S^T and dP^T
-// over its half, and swaps them with the partner through LDS. P^T and dS^T then live on
-// the query lanes with per-lane LSE and delta, and dQ^T[half] += K^T[half] dS^T reads its
-// A operand with ds_read_b64_tr_b16 from the same row-major K tile that fed S^T. K and V
-// tiles are double-buffered in LDS via buffer loads that write LDS directly; the copies of
-// the next tile are spread over the S^T and dP^T chains.
+// MI355X design: D <= 256, one wave owns 32 query rows of one head and keeps its Q and dO
+// rows in VGPRs (B operands of S^T = K Q^T and dP^T = V dO^T, lane = query). D = 512, a wave
+// pair owns them and splits the work by role: role 0 keeps the Q rows and runs S^T, role 1
+// keeps the dO rows, computes delta and runs dP^T (starting from -delta), both over the full
+// head dim; they swap the two results through LDS (one f32x16 each way) and each
+// accumulates its head-dim half of dQ^T. P^T and dS^T then live on the query lanes with
+// per-lane LSE, and dQ^T += K^T dS^T reads its A operand with ds_read_b64_tr_b16 from the
+// same row-major K tile that fed S^T. K and V tiles are double-buffered in LDS via buffer
+// loads that write LDS directly; the copies of the next tile are spread over the chains.
 #include "gfa_common.h"
 #include "gfa_params.h"
 #include "gfa_launch.h"
@@ -23,13 +24,13 @@ namespace gfa {
 
 template <int D, int BKV, bool IS_BF16, int NW, int SPLIT>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p) {
-  constexpr int DH = D / SPLIT;  // head-dim slice of one wave
-  constexpr int KTH = DH / 16;
+  constexpr int DH = D / SPLIT;  // head-dim slice of dQ^T one wave accumulates
+  constexpr int KT = D / 16;     // k-steps of a score chain (always the full head dim)
   constexpr int DBH = DH / 32;
   constexpr int SB = BKV / 32;
   constexpr int TILE = BKV * D * 2;
   constexpr int XHALF = SB * 16 * 64 * 4;              // one f32x16 per score block per lane
-  constexpr int XCH = SPLIT == 2 ? 2 * XHALF : 0;     // S^T and dP^T partials of a pair
+  constexpr int XCH = SPLIT == 2 ? 2 * XHALF : 0;     // S^T and dP^T of one pair
   static_assert(BKV % 32 == 0, "BKV must be a multiple of 32");
   static_assert(SPLIT == 1 || SPLIT == 2, "one wave or a wave pair per 32 query rows");
   static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
@@ -44,7 +45,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
-  __shared__ __attribute__((aligned(1024))) char xch_raw[NW * XCH > 0 ? NW * XCH : 16];
+  __shared__ __attribute__((aligned(1024))) char xch_raw[XCH > 0 ? (NW / 2) * XCH : 16];
   char GFA_LDS* const K0 = (char GFA_LDS*)k_lds0;
   char GFA_LDS* const K1 = (char GFA_LDS*)k_lds1;
   char GFA_LDS* const V0 = (char GFA_LDS*)v_lds0;
@@ -54,6 +55,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int unit = wave / SPLIT;
+  // Pair (SPLIT == 2): role 0 runs S^T = K Q^T, role 1 dP^T = V dO^T, each over the full head
+  // dim; they swap the results and each accumulates its head-dim half dh = role of dQ^T.
   const int dh = SPLIT == 2 ? (wave & 1) : 0;
   const int h = lane >> 5;
   const int l32 = lane & 31;
@@ -109,52 +112,64 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     }
     vis = intersect(vis, clamp_n(slo[qrow], p.N), clamp_n(shi[qrow], p.N));
   }
-  // ---- Q and dO halves (B operands), resident; delta prologue ----
-  i16x8 qf[KTH], df[KTH];
+  // ---- B operands of the score chains, resident; delta ----
+  // One wave: Q and dO rows (full head dim). Pair: role 0 the Q rows, role 1 the dO rows;
+  // role 1 also computes delta (it starts its dP^T chain from -delta, so role 0 never needs
+  // delta itself).
+  i16x8 qf[KT];                      // Q rows (one wave / role 0) or dO rows (role 1)
+  i16x8 df[SPLIT == 1 ? KT : 1];     // dO rows (one wave)
   float dpart = 0.f;
   {
-    const uint16_t* qr = p.q + (int64_t)b * p.qv.sb + (int64_t)head * p.qv.sh + (int64_t)qrow * p.qv.sn + dh * DH + 8 * h;
-    const uint16_t* dr = p.dout + (int64_t)b * p.dov.sb + (int64_t)head * p.dov.sh + (int64_t)qrow * p.dov.sn + dh * DH + 8 * h;
-    const uint16_t* orow = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh + (int64_t)qrow * p.ov.sn + dh * DH + 8 * h;
+    const uint16_t* qr = p.q + (int64_t)b * p.qv.sb + (int64_t)head * p.qv.sh + (int64_t)qrow * p.qv.sn + 8 * h;
+    const uint16_t* dr = p.dout + (int64_t)b * p.dov.sb + (int64_t)head * p.dov.sh + (int64_t)qrow * p.dov.sn + 8 * h;
+    const uint16_t* orow = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh + (int64_t)qrow * p.ov.sn + 8 * h;
+    if constexpr (SPLIT == 1) {
 #pragma unroll
-    for (int kk = 0; kk < KTH; ++kk) {
-      qf[kk] = *reinterpret_cast<const i16x8*>(qr + 16 * kk);
-      df[kk] = *reinterpret_cast<const i16x8*>(dr + 16 * kk);
-      const i16x8 of = *reinterpret_cast<const i16x8*>(orow + 16 * kk);
+      for (int kk = 0; kk < KT; ++kk) {
+        qf[kk] = *reinterpret_cast<const i16x8*>(qr + 16 * kk);
+        df[kk] = *reinterpret_cast<const i16x8*>(dr + 16 * kk);
+        const i16x8 of = *reinterpret_cast<const i16x8*>(orow + 16 * kk);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dpart += from16<IS_BF16>(df[kk][e]) * from16<IS_BF16>(of[e]);
+        for (int e = 0; e < 8; ++e) dpart += from16<IS_BF16>(df[kk][e]) * from16<IS_BF16>(of[e]);
+      }
+    } else {
+      const uint16_t* br = dh == 0 ? qr : dr;
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) qf[kk] = *reinterpret_cast<const i16x8*>(br + 16 * kk);
+      if (dh == 1) {
+#pragma unroll
+        for (int kk = 0; kk < KT; ++kk) {
+          const i16x8 of = *reinterpret_cast<const i16x8*>(orow + 16 * kk);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dpart += from16<IS_BF16>(qf[kk][e]) * from16<IS_BF16>(of[e]);
+        }
+      }
     }
   }
 #pragma unroll
-  for (int kk = 0; kk < KTH; ++kk) {
-    pin_vgpr(qf[kk]);
-    pin_vgpr(df[kk]);
+  for (int kk = 0; kk < KT; ++kk) pin_vgpr(qf[kk]);
+  if constexpr (SPLIT == 1) {
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) pin_vgpr(df[kk]);
   }
-  dpart = halves_sum(dpart);
-  float delta = dpart;
-  if constexpr (SPLIT == 2) {
-    // Pair exchange of the two head-dim halves of delta (through the exchange area).
-    *reinterpret_cast<float GFA_LDS*>(xch + wave * XCH + lane * 4) = dpart;
-    barrier_lds();
-    delta += *reinterpret_cast<const float GFA_LDS*>(xch + (wave ^ 1) * XCH + lane * 4);
-  }
+  const float delta = halves_sum(dpart);
   // Written for every row of an active block, also the rows past N in the last one (they
   // repeat row N-1's value): the dK/dV kernel reads whole 32-row tiles of delta and relies
   // on them being finite (its dS = P (dP - delta) with P = 0 on those rows).
-  if (active && dh == 0 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.lse_ld + q] = delta;
+  if (active && dh == SPLIT - 1 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.lse_ld + q] = delta;
   const float lse_log2 = p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + qrow] * kLog2e;
   // D >= 256: the dP^T chain starts from -delta (lane = query), so it yields dP - delta
   // directly and dS = P (dP - delta) costs one multiply (16 AGPRs, which the one-wave-per-SIMD
   // budget has; at D <= 128 they would cost an occupancy step, so the subtraction stays).
-  // With the head dim split over a pair, only the first half starts there (the partials are
-  // summed).
+  // In a pair only role 1 runs that chain.
   constexpr bool DP_FROM_DELTA = D >= 256;
   f32x16 neg_delta = f32x16{};
   if constexpr (DP_FROM_DELTA) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) neg_delta[r] = dh == 0 ? -delta : 0.f;
+    for (int r = 0; r < 16; ++r) neg_delta[r] = dh == SPLIT - 1 ? -delta : 0.f;
   }
   const float delta_left = DP_FROM_DELTA ? 0.f : delta;  // what dS still subtracts
+  if constexpr (DP_FROM_DELTA) pin_agpr(neg_delta);       // the chain's C operand lives there
 
   f32x16 acc[DBH];
 #pragma unroll
@@ -162,7 +177,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 
   int koff[8];
 #pragma unroll
-  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4) + dh * DH * 2;
+  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4);
   int toffA[4], toffB[4];  // K tile read transposed (A operand of dQ^T = K^T dS^T)
   {
     const int t16 = lane & 15;
@@ -176,16 +191,16 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       toffB[dl] = rB * (2 * D) + ((c ^ swz<D>(rB)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
     }
   }
-  char GFA_LDS* xmine = xch + wave * XCH + lane * 16;
-  const char GFA_LDS* xpart = xch + (wave ^ 1) * XCH + lane * 16;
+  // Pair exchange: slot 0 holds role 0's S^T, slot 1 role 1's dP^T - delta; both read both.
+  char GFA_LDS* xmine = xch + (wave >> 1) * XCH + dh * XHALF + lane * 16;
+  const char GFA_LDS* xs0 = xch + (wave >> 1) * XCH + lane * 16;
+  const char GFA_LDS* xs1 = xs0 + XHALF;
 
   const uint16_t* kbase = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh;
   const uint16_t* vbase = p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh;
   TileLoader<D, BKV, NW> kload, vload;
   kload.init(kbase, p.kv.sn, p.N, wave, lane);
   vload.init(vbase, p.vv.sn, p.N, wave, lane);
-
-  if constexpr (SPLIT == 2) barrier_lds();  // everyone has read the delta exchange before it is overwritten
 
   // One key tile: wait for it, then S^T = K Q^T and dP^T = V dO^T with the copies of tile
   // t+1 into the other buffers spread over the two chains (a run of copy issues would hold
@@ -202,25 +217,48 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     // No per-pair skip: a tile this pair cannot see is fully masked below, and the
     // straight-line body keeps the accumulators resident in registers.
     f32x16 s[SB], dp[SB];
-    s[0] = mma_chain1_lds_ld<IS_BF16, KTH, 4, NI>(kt, koff, 0, qf, [&](int i) { kload.load_part(i, rn, kn); });
-    __builtin_amdgcn_sched_barrier(0);
-    dp[0] = mma_chain1_lds_ld<IS_BF16, KTH, 4, NI>(vt, koff, 0, df, [&](int i) { vload.load_part(i, rn, vn); },
-                                                   neg_delta);
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (SPLIT == 1) {
+      s[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, NI>(kt, koff, 0, qf, [&](int i) { kload.load_part(i, rn, kn); });
+      __builtin_amdgcn_sched_barrier(0);
+      dp[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, NI>(vt, koff, 0, df, [&](int i) { vload.load_part(i, rn, vn); },
+                                                    neg_delta);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int sb = 1; sb < SB; ++sb) {
-      s[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(kt, koff, sb * 32 * (2 * D), qf);
-      dp[sb] = mma_chain1_lds<IS_BF16, KTH, 4>(vt, koff, sb * 32 * (2 * D), df) + neg_delta;
-    }
-    if constexpr (SPLIT == 2) {
+      for (int sb = 1; sb < SB; ++sb) {
+        s[sb] = mma_chain1_lds<IS_BF16, KT, 4>(kt, koff, sb * 32 * (2 * D), qf);
+        dp[sb] = mma_chain1_lds<IS_BF16, KT, 4>(vt, koff, sb * 32 * (2 * D), df) + neg_delta;
+      }
+    } else {
+      // This role's chain over the full head dim, with both tiles' copies spread over it;
+      // then the swap: each wave reads S^T and dP^T - delta from the exchange slots.
+      // The tile is picked by a (wave-uniform) branch, not a pointer select: each path then
+      // reads a statically named LDS object, which lets the compiler's wait insertion tell the
+      // reads from the in-flight copies (with a select it waits for the copies every product:
+      // 2.5x slower).
+      f32x16 own[SB];
+      auto run = [&](const char GFA_LDS* ct, const f32x16& init) __attribute__((always_inline)) {
+        own[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, 2 * NI>(ct, koff, 0, qf, [&](int i) {
+          if (i < NI) {
+            kload.load_part(i, rn, kn);
+          } else {
+            vload.load_part(i - NI, rn, vn);
+          }
+        }, init);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int sb = 1; sb < SB; ++sb) own[sb] = mma_chain1_lds<IS_BF16, KT, 4>(ct, koff, sb * 32 * (2 * D), qf) + init;
+      };
+      if (dh == 0) {
+        run(kt, f32x16{});
+      } else {
+        run(vt, neg_delta);
+      }
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const f32x4 vs = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
-          const f32x4 vd = {dp[sb][4 * j], dp[sb][4 * j + 1], dp[sb][4 * j + 2], dp[sb][4 * j + 3]};
-          *reinterpret_cast<f32x4 GFA_LDS*>(xmine + (sb * 4 + j) * 1024) = vs;
-          *reinterpret_cast<f32x4 GFA_LDS*>(xmine + XHALF + (sb * 4 + j) * 1024) = vd;
+          const f32x4 v4 = {own[sb][4 * j], own[sb][4 * j + 1], own[sb][4 * j + 2], own[sb][4 * j + 3]};
+          *reinterpret_cast<f32x4 GFA_LDS*>(xmine + (sb * 4 + j) * 1024) = v4;
         }
       }
       barrier_lds();
@@ -228,12 +266,12 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const f32x4 vs = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + (sb * 4 + j) * 1024);
-          const f32x4 vd = *reinterpret_cast<const f32x4 GFA_LDS*>(xpart + XHALF + (sb * 4 + j) * 1024);
+          const f32x4 vs = *reinterpret_cast<const f32x4 GFA_LDS*>(xs0 + (sb * 4 + j) * 1024);
+          const f32x4 vd = *reinterpret_cast<const f32x4 GFA_LDS*>(xs1 + (sb * 4 + j) * 1024);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            s[sb][4 * j + e] = s[sb][4 * j + e] + vs[e];
-            dp[sb][4 * j + e] = dp[sb][4 * j + e] + vd[e];
+            s[sb][4 * j + e] = vs[e];
+            dp[sb][4 * j + e] = vd[e];
           }
         }
       }
