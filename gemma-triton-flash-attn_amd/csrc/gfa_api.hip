@@ -409,9 +409,12 @@ int scratch_on(hipStream_t stream, void** out) {
       return fail(GFA_ERR_LAUNCH, "hipSetDevice(%d) failed: %s", dev, hipGetErrorString(err));
     void* p = nullptr;
     err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (cur != dev) hipSetDevice(cur);
+    const hipError_t restore = cur != dev ? hipSetDevice(cur) : hipSuccess;  // the caller's device again
     if (err != hipSuccess || p == nullptr)
       return fail(GFA_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(err));
+    if (restore != hipSuccess)
+      return fail(GFA_ERR_LAUNCH, "hipSetDevice(%d) restoring the caller's device failed: %s", cur,
+                  hipGetErrorString(restore));
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
