@@ -41,7 +41,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   constexpr int DB = D / 32;   // 32-row blocks of the dV^T / dK^T accumulator
   constexpr int SB = BQ / 32;  // 32-query score blocks per tile
   constexpr int TILE = BQ * D * 2;
-  constexpr int PX = ROLES == 2 ? SB * 64 * 64 : 0;  // fp32 P hand-off of one pair
+  // Pair at D=512: the two roles share the softmax work (see the tile step); at D=128, with
+  // three waves per SIMD filling each other's idle time, role 0 computes P alone and hands
+  // it over (the shared form measured 9% slower there, 3% faster at D=512).
+  constexpr bool SHARED = ROLES == 2 && D == 512;
+  // Pair exchange area per 32-query score block: shared, four 2 KB slots (S and dP halves,
+  // then P and dS halves); otherwise one fp32 P block. One f32x4 per lane per 1 KB plane.
+  constexpr int PX = ROLES == 2 ? SB * (SHARED ? 4 * 2048 : 4096) : 0;
   constexpr int NU = NW / ROLES;                     // 32-key units per workgroup
   constexpr int NS = 3 - ROLES;                      // stationary operands / accumulators per wave
   static_assert(ROLES == 1 || ROLES == 2, "one wave or a role-split pair per 32 keys");
@@ -57,7 +63,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   const int role = ROLES == 2 ? (wave & 1) : 0;  // pair: 0 = S, P and dV;  1 = dP, dS and dK
   const int h = lane >> 5;
   const int l32 = lane & 31;
-  char GFA_LDS* px = smem + 4 * TILE + unit * PX + lane * 16;
+  char GFA_LDS* px = smem + 4 * TILE + unit * PX + lane * 16;  // 1 KB planes of one f32x4 per lane
 
   // ---- workgroup -> (key block, split, b, kv head) ----
   // Heaviest first: under causal masking the early key blocks own the longest query
@@ -197,10 +203,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   dload.init(p.dout, p.dov.sn, p.N, wave, lane);
   const uint16_t* q_kv = p.q + (int64_t)b * p.qv.sb + (int64_t)kvh * p.R * p.qv.sh;
   const uint16_t* d_kv = p.dout + (int64_t)b * p.dov.sb + (int64_t)kvh * p.R * p.dov.sh;
-  // Row statistics this wave needs: st[0] = LSE (role 0) or delta (role 1); single wave:
-  // st[0] = LSE, st[1] = delta.
+  // Row statistics this wave needs. Single wave: st[0][sb][g] = LSE, st[1][sb][g] = delta of
+  // rows 8g + 4h + 0..3. Pair, shared form: each role turns half of the rows (g = 2 role,
+  // 2 role + 1) into P and dS: st[0][sb][0..1] = their LSE, st[0][sb][2..3] = their delta.
+  // Pair, hand-off form: st[0] = LSE (role 0) or delta (role 1) of all rows.
   const int64_t stat_off = ((int64_t)b * p.Hq + (int64_t)kvh * p.R) * p.lse_ld;
-  const float* stat_kv0 = (role == 0 ? p.lse : p.delta) + stat_off;
+  const float* stat_kv0 = p.lse + stat_off;
   const float* stat_kv1 = p.delta + stat_off;
 
   // Iteration `it` covers head kvh*R + r of query tile qt, it = (qt_hi - 1 - qt) * R + r:
@@ -289,27 +297,106 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (role == 0) {
-        make_p(s, st[0], q0);
-#pragma unroll
-        for (int sb = 0; sb < SB; ++sb) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const f32x4 v = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
-            *reinterpret_cast<f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024) = v;
+      if constexpr (SHARED) {
+        // Shared softmax: role RO turns the rows of registers 8 RO .. 8 RO + 7 (g = 2 RO,
+        // 2 RO + 1) into P and dS. Each role first hands its partner the half of its own chain
+        // result the partner needs (role 0: S of registers 8..15; role 1: dP of 0..7), then
+        // each hands back the half the partner accumulates (role 1: P of 8..15 for dV; role 0:
+        // dS of 0..7 for dK). Exchange slots of one score block: 0 S half, 1 dP half, 2 P
+        // half, 3 dS half (two 1 KB planes of f32x4 each). Split this way neither wave waits
+        // for the other's exponentials or dS; with P computed by role 0 alone, role 1 sat out
+        // about 20% of each step.
+        const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
+        auto slot = [&](int sb, int k, int j) __attribute__((always_inline)) { return pxr + (sb * 4 + k) * 2048 + j * 1024; };
+        auto shared = [&](auto ro) __attribute__((always_inline)) {
+          constexpr int RO = decltype(ro)::value;
+          constexpr int MH = 8 * RO, OH = 8 * (1 - RO);
+  #pragma unroll
+          for (int sb = 0; sb < SB; ++sb) {
+  #pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const f32x4 v = {s[sb][OH + 4 * j], s[sb][OH + 4 * j + 1], s[sb][OH + 4 * j + 2], s[sb][OH + 4 * j + 3]};
+              *reinterpret_cast<f32x4 GFA_LDS*>(slot(sb, RO, j)) = v;
+            }
+          }
+          barrier_lds();  // both halves of both chains are in the slots
+          float mine[SB][8];  // role 0: P of its half; role 1: dS of its half
+  #pragma unroll
+          for (int sb = 0; sb < SB; ++sb) {
+            f32x4 w[2];
+  #pragma unroll
+            for (int j = 0; j < 2; ++j) w[j] = *reinterpret_cast<const f32x4 GFA_LDS*>(slot(sb, 1 - RO, j));
+            float pv[8], dsv[8];
+  #pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float sv = RO == 0 ? s[sb][MH + i] : w[i >> 2][i & 3];
+              pv[i] = fast_exp2(sv * p.scale_log2 - st[0][sb][i >> 2][i & 3] * kLog2e);
+            }
+            if (need_mask) {
+  #pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                const int qi = q0 + sb * 32 + 8 * (2 * RO + (i >> 2)) + 4 * h + (i & 3);
+                pv[i] = vis.has(qi) ? pv[i] : 0.f;
+              }
+            }
+  #pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float dpv = RO == 1 ? s[sb][MH + i] : w[i >> 2][i & 3];
+              dsv[i] = pv[i] * (dpv - st[0][sb][2 + (i >> 2)][i & 3]);
+            }
+            // hand back what the partner accumulates: role 0 its dS half, role 1 its P half
+  #pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const f32x4 v = RO == 0 ? f32x4{dsv[4 * j], dsv[4 * j + 1], dsv[4 * j + 2], dsv[4 * j + 3]}
+                                      : f32x4{pv[4 * j], pv[4 * j + 1], pv[4 * j + 2], pv[4 * j + 3]};
+              *reinterpret_cast<f32x4 GFA_LDS*>(slot(sb, RO == 0 ? 3 : 2, j)) = v;
+            }
+  #pragma unroll
+            for (int i = 0; i < 8; ++i) mine[sb][i] = RO == 0 ? pv[i] : dsv[i];
+          }
+          barrier_lds();  // the halves handed back are in the slots
+  #pragma unroll
+          for (int sb = 0; sb < SB; ++sb) {
+  #pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const f32x4 w = *reinterpret_cast<const f32x4 GFA_LDS*>(slot(sb, RO == 0 ? 2 : 3, j));
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) s[sb][OH + 4 * j + e] = w[e];
+            }
+  #pragma unroll
+            for (int i = 0; i < 8; ++i) s[sb][MH + i] = mine[sb][i];
+          }
+        };
+        if (role == 0) {
+          shared(std::integral_constant<int, 0>{});
+        } else {
+          shared(std::integral_constant<int, 1>{});
+        }
+      } else {
+        // Hand-off form: role 0 computes P of all rows and hands it to role 1 (fp32).
+        if (role == 0) {
+          make_p(s, st[0], q0);
+  #pragma unroll
+          for (int sb = 0; sb < SB; ++sb) {
+  #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const f32x4 v = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
+              *reinterpret_cast<f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024) = v;
+            }
+          }
+        }
+        barrier_lds();  // P of this tile is in px
+        if (role == 1) {
+  #pragma unroll
+          for (int sb = 0; sb < SB; ++sb) {
+            f32x4 pv4[4];
+  #pragma unroll
+            for (int j = 0; j < 4; ++j) pv4[j] = *reinterpret_cast<const f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024);
+            make_ds(s[sb], pv4, st[0][sb]);
           }
         }
       }
-      barrier_lds();  // P of this tile is in px
-      if (role == 1) {
-#pragma unroll
-        for (int sb = 0; sb < SB; ++sb) {
-          f32x4 pv4[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) pv4[j] = *reinterpret_cast<const f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024);
-          make_ds(s[sb], pv4, st[0][sb]);
-        }
-      }
+      // s now holds P (role 0) or dS (role 1) for all 32 queries.
       i16x8 pb[BQ / 16];
       pack(s, pb);
       __builtin_amdgcn_sched_barrier(0);
@@ -371,13 +458,26 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     // Row statistics of this tile (rows q0 + sb*32 + 8g + 4h + 0..3; rows padded to a
     // multiple of 64), issued before the prefetch so they are not queued behind it.
     f32x4 st[NS][SB][4];
-#pragma unroll
-    for (int i = 0; i < NS; ++i) {
-      const float* srow = (i == 0 ? stat_kv0 : stat_kv1) + (int64_t)r_c * p.lse_ld + q0 + 4 * h;
+    if constexpr (SHARED) {
+      const int64_t roff = (int64_t)r_c * p.lse_ld + q0 + 4 * h + 16 * role;
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) st[i][sb][g] = *reinterpret_cast<const f32x4*>(srow + sb * 32 + 8 * g);
+        for (int j = 0; j < 2; ++j) {
+          st[0][sb][j] = *reinterpret_cast<const f32x4*>(stat_kv0 + roff + sb * 32 + 8 * j);
+          st[0][sb][2 + j] = *reinterpret_cast<const f32x4*>(stat_kv1 + roff + sb * 32 + 8 * j);
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        // pair (hand-off form): LSE for role 0, delta for role 1
+        const float* sbase = (ROLES == 2 && role == 1) || i == 1 ? stat_kv1 : stat_kv0;
+        const float* srow = sbase + (int64_t)r_c * p.lse_ld + q0 + 4 * h;
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) st[i][sb][g] = *reinterpret_cast<const f32x4*>(srow + sb * 32 + 8 * g);
+      }
     }
     // Next tile; the last iteration re-fetches its own tile into the idle buffer (never
     // read) so the loop body stays branch-free.
