@@ -22,6 +22,11 @@
 
 namespace gfa {
 
+// One wave per 32 rows at D >= 128 stages its rows (and its dQ rows) through LDS in whole-row
+// copies. At D = 64 three workgroups share a CU and hide the per-lane loads' latency; staging
+// there only adds a barrier and a round trip (measured 0.7% slower).
+constexpr bool dq_stages_rows(int D, int split) { return split == 1 && D >= 128; }
+
 template <int D, int BKV, bool IS_BF16, int NW, int SPLIT>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p) {
   constexpr int DH = D / SPLIT;  // head-dim slice of dQ^T one wave accumulates
@@ -36,6 +41,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
   // The swizzle permutes 16-chunk groups, so a head-dim half must be whole groups.
   static_assert(SPLIT == 1 || DH % 128 == 0, "a head-dim split needs halves of 128 or more elements");
+  constexpr bool STAGE = dq_stages_rows(D, SPLIT);
+  static_assert(!STAGE || NW == 4, "each wave stages its Q rows in one of four tile buffers");
 
   // Four distinct LDS tile objects (not one array indexed by a buffer id): with the loop
   // unrolled by two every access names its buffer statically, so the compiler's wait
@@ -46,6 +53,12 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
   __shared__ __attribute__((aligned(1024))) char xch_raw[XCH > 0 ? (NW / 2) * XCH : 16];
+  // STAGE: each wave stages its dO rows, then its O rows, and at the end its dQ rows in its
+  // TILE-byte block of this launch-sized array (its Q rows go to one of the tile buffers, idle
+  // before the loop). Dynamic, so the compiler's occupancy estimate (static LDS only) is that of
+  // the tile buffers: declared static, the 4 * TILE more bytes lower it, and the loop is then
+  // scheduled into a larger register set with extra AGPR copies per step.
+  extern __shared__ __attribute__((aligned(1024))) char stage_raw[];
   char GFA_LDS* const K0 = (char GFA_LDS*)k_lds0;
   char GFA_LDS* const K1 = (char GFA_LDS*)k_lds1;
   char GFA_LDS* const V0 = (char GFA_LDS*)v_lds0;
@@ -68,7 +81,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   lid /= p.Hkv;
   const int b = lid % p.B;
   lid /= p.B;
-  const int qsb = p.causal ? (p.g.n_qsb - 1 - lid) : lid;
+  // Full causal: longest rows first. Sliding window: nearly every block has the same key
+  // range, so the short first blocks (queries below the window) go first; they end at
+  // staggered times and spread the later blocks' prologues (row copies) over time instead of
+  // every CU loading its rows at once.
+  const int qsb = (p.causal && p.window <= 0) ? (p.g.n_qsb - 1 - lid) : lid;
 
   const int head = kvh * p.R + hg * p.g.hpw + (unit % p.g.hpw);
   const int q0 = (qsb * p.g.qbw + unit / p.g.hpw) * 32;
@@ -112,36 +129,80 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     }
     vis = intersect(vis, clamp_n(slo[qrow], p.N), clamp_n(shi[qrow], p.N));
   }
+  int koff[8];
+#pragma unroll
+  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4);
+
+  const uint16_t* kbase = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh;
+  const uint16_t* vbase = p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh;
+  TileLoader<D, BKV, NW> kload, vload;
+  kload.init(kbase, p.kv.sn, p.N, wave, lane);
+  vload.init(vbase, p.vv.sn, p.N, wave, lane);
+
   // ---- B operands of the score chains, resident; delta ----
-  // One wave: Q and dO rows (full head dim). Pair: role 0 the Q rows, role 1 the dO rows;
-  // role 1 also computes delta (it starts its dP^T chain from -delta, so role 0 never needs
-  // delta itself).
+  // One wave: Q and dO rows (full head dim); STAGE: staged through LDS by whole-row copies and
+  // read back in the operand layout, the first key tile's copies issued before the O rows are
+  // read for delta. Pair: role 0 the Q rows, role 1 the dO rows (loaded per lane; the D = 512
+  // pair's prologue is a small part of its blocks); role 1 also computes delta (it starts its
+  // dP^T chain from -delta, so role 0 never needs delta itself).
+  // The row's LSE first: its load then overlaps the row copies.
+  const float lse_log2 = p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + qrow] * kLog2e;
   i16x8 qf[KT];                      // Q rows (one wave / role 0) or dO rows (role 1)
   i16x8 df[SPLIT == 1 ? KT : 1];     // dO rows (one wave)
   float dpart = 0.f;
   {
-    const uint16_t* qr = p.q + (int64_t)b * p.qv.sb + (int64_t)head * p.qv.sh + (int64_t)qrow * p.qv.sn + 8 * h;
-    const uint16_t* dr = p.dout + (int64_t)b * p.dov.sb + (int64_t)head * p.dov.sh + (int64_t)qrow * p.dov.sn + 8 * h;
-    const uint16_t* orow = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh + (int64_t)qrow * p.ov.sn + 8 * h;
-    if constexpr (SPLIT == 1) {
+    const uint16_t* qb = p.q + (int64_t)b * p.qv.sb + (int64_t)head * p.qv.sh;
+    const uint16_t* db = p.dout + (int64_t)b * p.dov.sb + (int64_t)head * p.dov.sh;
+    const uint16_t* ob = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh;
+    if constexpr (STAGE) {
+      // Each wave's own blocks: Q in tile buffer `wave`, dO and then O in its stage block.
+      char GFA_LDS* qblk = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;
+      char GFA_LDS* sblk = (char GFA_LDS*)stage_raw + wave * TILE;
+      copy_rows_lds<D>(qb, p.qv.sn, p.N, q0, lane, qblk);
+      copy_rows_lds<D>(db, p.dov.sn, p.N, q0, lane, sblk);
+      drain_tile_copies();
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
-        qf[kk] = *reinterpret_cast<const i16x8*>(qr + 16 * kk);
-        df[kk] = *reinterpret_cast<const i16x8*>(dr + 16 * kk);
-        const i16x8 of = *reinterpret_cast<const i16x8*>(orow + 16 * kk);
+        qf[kk] = lds_read16(qblk, koff[kk & 7] + 256 * (kk >> 3));
+        df[kk] = lds_read16(sblk, koff[kk & 7] + 256 * (kk >> 3));
+      }
+      barrier_lds();  // every wave has read its Q block out of the tile buffers
+      copy_rows_lds<D>(ob, p.ov.sn, p.N, q0, lane, sblk);
+      if (t_lo < t_hi) {
+        kload.load(t_lo * BKV, K0);
+        vload.load(t_lo * BKV, V0);
+      }
+      drain_tile_copies();
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) {
+        const i16x8 of = lds_read16(sblk, koff[kk & 7] + 256 * (kk >> 3));
 #pragma unroll
         for (int e = 0; e < 8; ++e) dpart += from16<IS_BF16>(df[kk][e]) * from16<IS_BF16>(of[e]);
       }
     } else {
-      const uint16_t* br = dh == 0 ? qr : dr;
-#pragma unroll
-      for (int kk = 0; kk < KT; ++kk) qf[kk] = *reinterpret_cast<const i16x8*>(br + 16 * kk);
-      if (dh == 1) {
+      const uint16_t* qr = qb + (int64_t)qrow * p.qv.sn + 8 * h;
+      const uint16_t* dr = db + (int64_t)qrow * p.dov.sn + 8 * h;
+      const uint16_t* orow = ob + (int64_t)qrow * p.ov.sn + 8 * h;
+      if constexpr (SPLIT == 1) {
 #pragma unroll
         for (int kk = 0; kk < KT; ++kk) {
+          qf[kk] = *reinterpret_cast<const i16x8*>(qr + 16 * kk);
+          df[kk] = *reinterpret_cast<const i16x8*>(dr + 16 * kk);
           const i16x8 of = *reinterpret_cast<const i16x8*>(orow + 16 * kk);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) dpart += from16<IS_BF16>(qf[kk][e]) * from16<IS_BF16>(of[e]);
+          for (int e = 0; e < 8; ++e) dpart += from16<IS_BF16>(df[kk][e]) * from16<IS_BF16>(of[e]);
+        }
+      } else {
+        const uint16_t* br = dh == 0 ? qr : dr;
+#pragma unroll
+        for (int kk = 0; kk < KT; ++kk) qf[kk] = *reinterpret_cast<const i16x8*>(br + 16 * kk);
+        if (dh == 1) {
+#pragma unroll
+          for (int kk = 0; kk < KT; ++kk) {
+            const i16x8 of = *reinterpret_cast<const i16x8*>(orow + 16 * kk);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dpart += from16<IS_BF16>(qf[kk][e]) * from16<IS_BF16>(of[e]);
+          }
         }
       }
     }
@@ -152,12 +213,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) pin_vgpr(df[kk]);
   }
-  const float delta = halves_sum(dpart);
-  // Written for every row of an active block, also the rows past N in the last one (they
-  // repeat row N-1's value): the dK/dV kernel reads whole 32-row tiles of delta and relies
-  // on them being finite (its dS = P (dP - delta) with P = 0 on those rows).
-  if (active && dh == SPLIT - 1 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.lse_ld + q] = delta;
-  const float lse_log2 = p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + qrow] * kLog2e;
+  const float delta = halves_sum(dpart);  // stored after the loop
   // D >= 256: the dP^T chain starts from -delta (lane = query), so it yields dP - delta
   // directly and dS = P (dP - delta) costs one multiply (16 AGPRs, which the one-wave-per-SIMD
   // budget has; at D <= 128 they would cost an occupancy step, so the subtraction stays).
@@ -175,9 +231,6 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 #pragma unroll
   for (int i = 0; i < DBH; ++i) acc[i] = f32x16{};
 
-  int koff[8];
-#pragma unroll
-  for (int kl = 0; kl < 8; ++kl) koff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4);
   int toffA[4], toffB[4];  // K tile read transposed (A operand of dQ^T = K^T dS^T)
   {
     const int t16 = lane & 15;
@@ -195,12 +248,6 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   char GFA_LDS* xmine = xch + (wave >> 1) * XCH + dh * XHALF + lane * 16;
   const char GFA_LDS* xs0 = xch + (wave >> 1) * XCH + lane * 16;
   const char GFA_LDS* xs1 = xs0 + XHALF;
-
-  const uint16_t* kbase = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh;
-  const uint16_t* vbase = p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh;
-  TileLoader<D, BKV, NW> kload, vload;
-  kload.init(kbase, p.kv.sn, p.N, wave, lane);
-  vload.init(vbase, p.vv.sn, p.N, wave, lane);
 
   // One key tile: wait for it, then S^T = K Q^T and dP^T = V dO^T with the copies of tile
   // t+1 into the other buffers spread over the two chains (a run of copy issues would hold
@@ -309,7 +356,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     for (int db = 0; db < DBH; ++db) pin_agpr(acc[db]);
   };
 
-  if (t_lo < t_hi) {
+  if (!STAGE && t_lo < t_hi) {  // STAGE: issued in the prologue
     kload.load(t_lo * BKV, K0);
     vload.load(t_lo * BKV, V0);
   }
@@ -321,7 +368,38 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   }
   drain_tile_copies();
 
-  if (active && q < p.N) {
+  // Delta is stored here, not after the prologue: a store there would hold up the first tile
+  // barrier (its vmcnt wait covers stores too). Written for every row of an active block, also
+  // the rows past N in the last one (they repeat row N-1's value): the dK/dV kernel reads whole
+  // 32-row tiles of delta and relies on them being finite (its dS = P (dP - delta) with P = 0
+  // on those rows).
+  if (active && dh == SPLIT - 1 && h == 0) p.delta[((int64_t)b * p.Hq + head) * p.lse_ld + q] = delta;
+  if constexpr (STAGE) {
+    // dQ rows through this wave's stage block (idle since the prologue; laid out like a tile),
+    // then whole rows to HBM: per-lane stores of 4 elements straight from the accumulator
+    // layout touch 32 rows per instruction and hold the block's end up.
+    char GFA_LDS* sblk = (char GFA_LDS*)stage_raw + wave * TILE;
+    // The lane index, opaque from here: the epilogue's addresses are then computed here, not
+    // shared with the prologue's (which would keep them live, in AGPR copies, over the loop).
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int r32 = ln & 31;
+    const int hh = ln >> 5;
+#pragma unroll
+    for (int db = 0; db < DBH; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        i16x4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[db][4 * g + e] * p.scale);
+        const int c = 4 * db + g;  // 16-byte chunk of row l32 that holds these 4 + 4 elements
+        *reinterpret_cast<i16x4 GFA_LDS*>(sblk + r32 * (2 * D) + ((c ^ swz<D>(r32)) << 4) + 8 * hh) = o4;
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one block at a time (else every accumulator is read out first)
+    }
+    store_rows_lds<D>(p.dq + (int64_t)b * p.dqv.sb + (int64_t)head * p.dqv.sh, p.dqv.sn, active ? p.N : 0, q0, ln,
+                      sblk);
+  } else if (active && q < p.N) {
     uint16_t* dqrow = p.dq + (int64_t)b * p.dqv.sb + (int64_t)head * p.dqv.sh + (int64_t)q * p.dqv.sn + dh * DH;
 #pragma unroll
     for (int db = 0; db < DBH; ++db) {
@@ -348,7 +426,8 @@ template __global__ void bwd_dq_kernel<64, 32, false, 4, 1>(const BwdDqParams);
 
 template <int D, int BKV, bool IS_BF16, int NW, int SPLIT>
 static hipError_t launch_dq_t(const BwdDqParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
+  const unsigned stage_bytes = dq_stages_rows(D, SPLIT) ? NW * BKV * D * 2 : 0;  // the kernel's stage_raw
+  hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT>), dim3(p.g.nblocks), dim3(NW * 64), stage_bytes, stream, p);
   return hipGetLastError();
 }
 

@@ -236,6 +236,47 @@ struct TileLoader {
   }
 };
 
+// One wave copies rows [row0, row0 + 32) of a (batch, head) slice into an LDS block laid out
+// like a TileLoader tile (row-major, chunk c of row r at position c ^ swz(r)), rows past
+// n_rows repeating row n_rows - 1. Each of the D/16 direct global->LDS copies covers whole
+// rows (1 KB, coalesced); loading the same rows straight into the MFMA operand layout (lane =
+// row) touches 32 rows per instruction and is several times slower. The caller waits for
+// vmcnt before reading the block.
+template <int D>
+__device__ __forceinline__ void copy_rows_lds(const uint16_t* base, int64_t row_stride, int n_rows, int row0, int lane,
+                                              char GFA_LDS* blk) {
+  constexpr int CPR = D / 8;
+  constexpr int RPI = 64 / CPR;
+  const __amdgpu_buffer_rsrc_t rs = slice_rsrc(base, row_stride, n_rows, D);
+  const unsigned sb = (unsigned)(row_stride * 2);
+  const int lrow = lane / CPR;
+  const int lc = lane % CPR;
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int r = i * RPI + lrow;
+    const unsigned vo = (unsigned)min(row0 + r, n_rows - 1) * sb + (unsigned)((lc ^ swz<D>(r)) << 4);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void GFA_LDS*)(blk + i * 1024), 16, vo, 0, 0, 0);
+  }
+}
+
+// The reverse of copy_rows_lds: one wave writes rows [row0, row0 + 32) of a (batch, head)
+// slice from an LDS block in the same layout, skipping rows at or past n_rows; each store
+// instruction covers whole rows (16 bytes per lane).
+template <int D>
+__device__ __forceinline__ void store_rows_lds(uint16_t* base, int64_t row_stride, int n_rows, int row0, int lane,
+                                               const char GFA_LDS* blk) {
+  constexpr int CPR = D / 8;
+  constexpr int RPI = 64 / CPR;
+  const int lrow = lane / CPR;
+  const int lc = lane % CPR;
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int r = i * RPI + lrow;
+    const i16x8 v = lds_read16(blk, i * 1024 + lrow * (2 * D) + ((lc ^ swz<D>(r)) << 4));
+    if (row0 + r < n_rows) *reinterpret_cast<i16x8*>(base + (int64_t)(row0 + r) * row_stride + 8 * lc) = v;
+  }
+}
+
 // Score block C(32 x 32) = sum_kk A_kk * B_kk over KT k-steps, where A_kk are rows of a
 // swizzled LDS tile (per-lane offsets koff[kk % 8] + 256 * (kk / 8) + extra) and B_kk are
 // register-resident fragments, as one chain of back-to-back dependent MFMAs (a second,
