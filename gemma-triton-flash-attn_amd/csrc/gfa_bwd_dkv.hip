@@ -35,6 +35,10 @@ namespace gfa {
 // used at D=256 and D=64, where that is faster than the pair. Role-split pairs run D=512
 // (one wave per SIMD) and D=128 (two). WPE: waves per SIMD the register budget is bounded
 // for.
+// One wave per 32 keys at D >= 128 stages its K / V rows (and its dK / dV rows) through LDS in
+// whole-row copies; per-lane loads in the MFMA operand layout touch 32 rows per instruction.
+constexpr bool dkv_stages_rows(int D, int roles) { return roles == 1 && D >= 128; }
+
 template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE>
 __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParams p) {
   constexpr int KT = D / 16;   // MFMA k-steps of the score products (full head dim)
@@ -54,8 +58,14 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   static_assert(BQ % 32 == 0, "BQ must be a multiple of 32");
   static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
 
+  constexpr bool STAGE = dkv_stages_rows(D, ROLES);
+
   __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NU * PX];
   char GFA_LDS* smem = (char GFA_LDS*)smem_raw;
+  // STAGE: each wave's TILE-byte block of this launch-sized array takes its V rows before the
+  // loop and its dV, then dK rows after it (its K rows go to one of the tile buffers). Dynamic,
+  // so the compiler's occupancy estimate (static LDS only) stays that of the tile buffers.
+  extern __shared__ __attribute__((aligned(1024))) char stage_raw[];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -80,7 +90,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   const int b = lid % p.B;
   lid /= p.B;
   const int split = lid % p.q_splits;
-  const int kb = (lid / p.q_splits) * 4 + kb_lo;
+  int kb = (lid / p.q_splits) * 4 + kb_lo;
+  // Sliding window: nearly every key block has the same query range, so the short last blocks
+  // (keys within a window of the end) go first; they end at staggered times and spread the
+  // later blocks' prologues instead of every CU loading its rows at once.
+  if (p.causal && p.window > 0) kb = (p.n_kb + 3) / 4 * 4 - 1 - kb;
   if (kb >= p.n_kb) return;  // whole workgroup, before any barrier
 
   const int wg_k0 = kb * NU * 32;
@@ -128,7 +142,25 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // ---- stationary B operands (lane = key, full head dim) ----
   // pair: sf[0] = K rows (role 0) or V rows (role 1);  single wave: sf[0] = K, sf[1] = V.
   i16x8 sf[NS][KT];
-  {
+  int roff[8];  // tile rows (A operand of S / dP): row l32, chunk 2*kk + h  (+256 * (kk >> 3))
+#pragma unroll
+  for (int kl = 0; kl < 8; ++kl) roff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4);
+  if constexpr (STAGE) {
+    // K rows into tile buffer `wave` (idle before the loop), V rows into the stage block, in
+    // whole-row copies; read back in the operand layout.
+    static_assert(NS == 2 && NU == 4, "one wave per 32 keys, four per workgroup");
+    char GFA_LDS* kblk = smem + wave * TILE;
+    char GFA_LDS* vblk = (char GFA_LDS*)stage_raw + wave * TILE;
+    copy_rows_lds<D>(p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh, p.kv.sn, p.N, k0, lane, kblk);
+    copy_rows_lds<D>(p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh, p.vv.sn, p.N, k0, lane, vblk);
+    drain_tile_copies();
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      sf[0][kk] = lds_read16(kblk, roff[kk & 7] + 256 * (kk >> 3));
+      sf[1][kk] = lds_read16(vblk, roff[kk & 7] + 256 * (kk >> 3));
+    }
+    barrier_lds();  // every wave has read its K rows out of the tile buffers
+  } else {
     const uint16_t* krp = p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh + (int64_t)krow * p.kv.sn + 8 * h;
     const uint16_t* vrp = p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh + (int64_t)krow * p.vv.sn + 8 * h;
 #pragma unroll
@@ -153,9 +185,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // The other head dims keep the tables (measured 2-4% faster there).
   constexpr bool ONE_BASE = D == 128;
   const int roff0 = l32 * (2 * D) + ((h ^ swz<D>(l32)) << 4);  // tile row l32, chunk h (k-step 0)
-  int roff[8];  // tile rows (A operand of S / dP): row l32, chunk 2*kk + h  (+256 * (kk >> 3))
-#pragma unroll
-  for (int kl = 0; kl < 8; ++kl) roff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4);
   int toff0;  // tiles read transposed (A operands of dV^T, dK^T): rows 4h + t/4, column block 0
   int toffA[4], toffB[4];
   {
@@ -500,7 +529,39 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   drain_tile_copies();
 
   // ---- epilogue: lane = key, registers = head-dim rows 32*db + 8*g + 4*h + e ----
-  if (active && key < p.N) {
+  if (STAGE && p.q_splits == 1) {
+    // dV, then dK rows through this wave's stage block (idle since the prologue; laid out like
+    // a tile), then whole rows to HBM. The lane index is made opaque here so the addresses are
+    // computed here, not shared with the prologue's (which keeps them live over the loop).
+    char GFA_LDS* sblk = (char GFA_LDS*)stage_raw + wave * TILE;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int r32 = ln & 31;
+    const int hh = ln >> 5;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const float osc = i == 0 ? 1.f : p.scale;  // dK carries the softmax scale
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          i16x4 o4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[i][db][4 * g + e] * osc);
+          const int c = 4 * db + g;  // 16-byte chunk of row r32 that holds these 4 + 4 elements
+          *reinterpret_cast<i16x4 GFA_LDS*>(sblk + r32 * (2 * D) + ((c ^ swz<D>(r32)) << 4) + 8 * hh) = o4;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (i == 0) {
+        store_rows_lds<D>(p.dv + (int64_t)b * p.dvv.sb + (int64_t)kvh * p.dvv.sh, p.dvv.sn, active ? p.N : 0, k0, ln,
+                          sblk);
+      } else {
+        store_rows_lds<D>(p.dk + (int64_t)b * p.dkv.sb + (int64_t)kvh * p.dkv.sh, p.dkv.sn, active ? p.N : 0, k0, ln,
+                          sblk);
+      }
+    }
+  } else if (active && key < p.N) {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int which = ROLES == 2 ? role : i;       // 0: dV, 1: dK
@@ -588,7 +649,9 @@ template __global__ void dkv_reduce_kernel<false>(const BwdDkvParams, int);
 
 template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE>
 static hipError_t launch_dkv_t(const BwdDkvParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW, ROLES, WPE>), dim3(p.nblocks), dim3(NW * 64), 0, stream, p);
+  const unsigned stage_bytes = dkv_stages_rows(D, ROLES) ? NW * BQ * D * 2 : 0;  // the kernel's stage_raw
+  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW, ROLES, WPE>), dim3(p.nblocks), dim3(NW * 64), stage_bytes, stream,
+                     p);
   return hipGetLastError();
 }
 
