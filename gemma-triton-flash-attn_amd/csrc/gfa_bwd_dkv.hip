@@ -19,7 +19,7 @@
 //   role 0: S = Q K^T (A = Q tile rows), P = exp2(S*scale*log2e - LSE*log2e) masked,
 //           P handed to the partner through LDS (fp32), then dV^T += dO^T P;
 //   role 1: dP = dO V^T (A = dO tile rows), dS = P (dP - delta), then dK^T += Q^T dS;
-// the dV^T / dK^T accumulators (32 keys x D, fp32) fill the AGPRs, and the A operands of
+// the dV^T / dK^T accumulators (32 keys x D, fp32) fill the AGPRs at D=512, and the A operands of
 // the two accumulations are read with ds_read_b64_tr_b16 from the same row-major tiles
 // that fed the score products. The only cross-wave traffic is the one-way P hand-off, and
 // no softmax work is duplicated. All R query heads of the KV head stream through the
@@ -32,9 +32,10 @@ namespace gfa {
 
 // ROLES = 2: a wave pair per 32 keys, split by role (see above). ROLES = 1: one wave per
 // 32 keys does all four products (K and V rows resident, dV^T and dK^T both in AGPRs);
-// used at D=256 and D=64, where that is faster than the pair. Role-split pairs run D=512
-// (one wave per SIMD) and D=128 (two). WPE: waves per SIMD the register budget is bounded
-// for.
+// used at D=64, and at D=256 without a window, where that is faster than the pair. Role-split
+// pairs run D=512 (one wave per SIMD), D=128 (two) and D=256 with a window (two, everything
+// in VGPRs: 64 keys per workgroup, two workgroups per CU). WPE: waves per SIMD the register
+// budget is bounded for.
 // One wave per 32 keys at D >= 128 stages its K / V rows (and its dK / dV rows) through LDS in
 // whole-row copies; per-lane loads in the MFMA operand layout touch 32 rows per instruction.
 constexpr bool dkv_stages_rows(int D, int roles) { return roles == 1 && D >= 128; }
@@ -183,7 +184,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // one base each: kstep_off and mma_tr_accumulate_b derive the others with an XOR next to
   // each read, where eight-entry offset tables would cost 14 registers (5% faster measured).
   // The other head dims keep the tables (measured 2-4% faster there).
-  constexpr bool ONE_BASE = D == 128;
+  constexpr bool ONE_BASE = D == 128 || (D == 256 && WPE == 2);
+  // Role pairs at two waves per SIMD and D=256 (register-bound): the score chains start from
+  // the row statistic instead of zero, so neither LSE nor delta stays live past the chain:
+  // role 0 from -LSE / scale (P = exp2(scale * log2e * acc)), role 1 from -delta (dS = P acc).
+  constexpr bool INIT = ROLES == 2 && !SHARED && D == 256;
   const int roff0 = l32 * (2 * D) + ((h ^ swz<D>(l32)) << 4);  // tile row l32, chunk h (k-step 0)
   int toff0;  // tiles read transposed (A operands of dV^T, dK^T): rows 4h + t/4, column block 0
   int toffA[4], toffB[4];
@@ -203,19 +208,21 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   }
   // Score chains (the first one of a step with NL tile-copy instructions spread over it) and
   // accumulations from tiles read transposed, in the offset form chosen above.
-  auto chain = [&](const char GFA_LDS* tile, int extra, const i16x8 (&bf)[KT]) __attribute__((always_inline)) {
+  auto chain = [&](const char GFA_LDS* tile, int extra, const i16x8 (&bf)[KT], const f32x16& c0 = f32x16{})
+                   __attribute__((always_inline)) {
     if constexpr (ONE_BASE) {
-      return mma_chain1_lds_b<IS_BF16, KT, 4, 1>(tile, roff0, extra, bf);
+      return mma_chain1_lds_b<IS_BF16, KT, 4, 1>(tile, roff0, extra, bf, c0);
     } else {
-      return mma_chain1_lds<IS_BF16, KT, 4, 1>(tile, roff, extra, bf);
+      return mma_chain1_lds<IS_BF16, KT, 4, 1>(tile, roff, extra, bf, c0);
     }
   };
-  auto chain_ld = [&](auto nl, const char GFA_LDS* tile, const i16x8 (&bf)[KT], auto&& ld) __attribute__((always_inline)) {
+  auto chain_ld = [&](auto nl, const char GFA_LDS* tile, const i16x8 (&bf)[KT], auto&& ld,
+                      const f32x16& c0 = f32x16{}) __attribute__((always_inline)) {
     constexpr int NL = decltype(nl)::value;
     if constexpr (ONE_BASE) {
-      return mma_chain1_lds_ld_b<IS_BF16, KT, 4, NL>(tile, roff0, 0, bf, ld);
+      return mma_chain1_lds_ld_b<IS_BF16, KT, 4, NL>(tile, roff0, 0, bf, ld, c0);
     } else {
-      return mma_chain1_lds_ld<IS_BF16, KT, 4, NL>(tile, roff, 0, bf, ld);
+      return mma_chain1_lds_ld<IS_BF16, KT, 4, NL>(tile, roff, 0, bf, ld, c0);
     }
   };
   auto accumulate = [&](f32x16 (&acc_)[DB], const char GFA_LDS* tile, const i16x8 (&bop)[BQ / 16])
@@ -240,13 +247,21 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   const float* stat_kv0 = p.lse + stat_off;
   const float* stat_kv1 = p.delta + stat_off;
 
-  // Iteration `it` covers head kvh*R + r of query tile qt, it = (qt_hi - 1 - qt) * R + r:
-  // query tiles from the last one down, the R heads of a tile back to back. Under causal
-  // masking every key block's range ends at the same last tile, so the workgroups that run
-  // together walk the same Q / dO tiles at the same time and share them in L2.
-  // (r_c, qt_c) walk it incrementally.
+  // Iteration `it` covers head kvh*R + r of query tile qt, the R heads of a tile back to back;
+  // (r_c, qt_c) walk it incrementally. Neighbouring key blocks of one KV head run together on
+  // one XCD, and the walk makes them read the same Q / dO tiles at the same time, so that the
+  // tiles come from L2:
+  // - causal: query tiles from the last one down, it = (qt_hi - 1 - qt) * R + r (every key
+  //   block's range ends at the same last tile);
+  // - sliding window: upward and cyclically inside [qt_lo, qt_hi), starting at the tile whose
+  //   index is a multiple of nqt, so that step j of every workgroup reads a tile with index
+  //   = j (mod nqt). Started at its own first (or last) tile, each key block ran a few tiles behind
+  //   its neighbour, and three quarters of the dK/dV kernel's tile reads missed L2 (HBM reads
+  //   3.7x this walk's; 3-5% slower).
+  const bool rotate = swa;
+  const int phase = rotate && nqt > 0 ? (nqt - qt_lo % nqt) % nqt : 0;
   int r_c = it_lo % p.R;
-  int qt_c = qt_hi - 1 - it_lo / p.R;
+  int qt_c = rotate ? qt_lo + (it_lo / p.R + phase) % max(nqt, 1) : qt_hi - 1 - it_lo / p.R;
   if (it_lo < it_hi) {
     qload.rebase(q_kv + (int64_t)r_c * p.qv.sh, p.qv.sn, p.N);
     dload.rebase(d_kv + (int64_t)r_c * p.dov.sh, p.dov.sn, p.N);
@@ -261,6 +276,25 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) sc[sb][r] = fast_exp2(sc[sb][r] * p.scale_log2 - lse[sb][r >> 2][r & 3] * kLog2e);
+    }
+    if (need_mask) {
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qi = q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          sc[sb][r] = vis.has(qi) ? sc[sb][r] : 0.f;
+        }
+      }
+    }
+  };
+  // P from a chain that started at -LSE / scale: exp2(scale * log2e * acc), masked.
+  auto make_p_init = [&](f32x16 (&sc)[SB], int q0) __attribute__((always_inline)) {
+    const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[sb][r] = fast_exp2(sc[sb][r] * p.scale_log2);
     }
     if (need_mask) {
 #pragma unroll
@@ -310,6 +344,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       const char GFA_LDS* ct = role == 0 ? qt : dt;
       const char GFA_LDS* tt = role == 0 ? dt : qt;
       f32x16 s[SB];
+      f32x16 c0[SB];
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+        c0[sb] = f32x16{};
+        if constexpr (INIT) {
+          const float f = role == 0 ? -p.inv_scale : -1.f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) c0[sb][r] = st[0][sb][r >> 2][r & 3] * f;
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);  // the MFMA pipelines are scheduled on their own
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
@@ -320,9 +364,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
             } else {
               dload.load_part(i - NI, row_n, dn);
             }
-          });
+          }, c0[sb]);
         } else {
-          s[sb] = chain(ct, sb * 32 * (2 * D), sf[0]);
+          s[sb] = chain(ct, sb * 32 * (2 * D), sf[0], c0[sb]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -404,7 +448,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       } else {
         // Hand-off form: role 0 computes P of all rows and hands it to role 1 (fp32).
         if (role == 0) {
-          make_p(s, st[0], q0);
+          if constexpr (INIT) {
+            make_p_init(s, q0);
+          } else {
+            make_p(s, st[0], q0);
+          }
   #pragma unroll
           for (int sb = 0; sb < SB; ++sb) {
   #pragma unroll
@@ -421,7 +469,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
             f32x4 pv4[4];
   #pragma unroll
             for (int j = 0; j < 4; ++j) pv4[j] = *reinterpret_cast<const f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024);
-            make_ds(s[sb], pv4, st[0][sb]);
+            if constexpr (INIT) {
+#pragma unroll
+              for (int r = 0; r < 16; ++r) s[sb][r] *= pv4[r >> 2][r & 3];  // dS = P (dP - delta)
+            } else {
+              make_ds(s[sb], pv4, st[0][sb]);
+            }
           }
         }
       }
@@ -472,7 +525,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     }
     // D >= 256: the accumulators fill the AGPRs and stay there. At D=64 everything fits the
     // VGPRs of two waves per SIMD; unpinned, the MFMAs write VGPRs directly (12% faster).
-    if constexpr (D >= 256) {
+    if constexpr (D >= 256 && WPE == 1) {
 #pragma unroll
       for (int i = 0; i < NS; ++i)
 #pragma unroll
@@ -513,7 +566,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     int r_n = r_c + 1, qt_n = qt_c;
     if (r_n == p.R) {
       r_n = 0;
-      --qt_n;
+      qt_n = rotate ? (qt_c + 1 == qt_hi ? qt_lo : qt_c + 1) : qt_c - 1;
     }
     if (it + 1 >= it_hi) {
       r_n = r_c;
@@ -641,6 +694,7 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const BwdDkvParams p, i
   template __global__ void bwd_dkv_kernel<DD, BB, false, WW, RR, EE>(const BwdDkvParams);
 GFA_DKV_INST(512, 32, 4, 2, 1)
 GFA_DKV_INST(256, 32, 4, 1, 1)
+GFA_DKV_INST(256, 32, 4, 2, 2)
 GFA_DKV_INST(64, 32, 4, 1, 2)
 GFA_DKV_INST(128, 32, 4, 2, 2)
 #undef GFA_DKV_INST
@@ -665,6 +719,7 @@ hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, int nw, int role
   }
   GFA_DKV_CASE(512, 32, 4, 2, 1)
   GFA_DKV_CASE(256, 32, 4, 1, 1)
+  GFA_DKV_CASE(256, 32, 4, 2, 2)
   GFA_DKV_CASE(64, 32, 4, 1, 2)
   GFA_DKV_CASE(128, 32, 4, 2, 2)
 #undef GFA_DKV_CASE

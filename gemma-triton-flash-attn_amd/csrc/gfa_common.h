@@ -286,9 +286,9 @@ __device__ __forceinline__ void store_rows_lds(uint16_t* base, int64_t row_strid
 // between two sched_barrier(0)).
 template <bool IS_BF16, int KT, int PF, int SG = 0>
 __device__ __forceinline__ f32x16 mma_chain1_lds(const char GFA_LDS* tile, const int (&koff)[8], int extra,
-                                                 const i16x8 (&bf)[KT]) {
+                                                 const i16x8 (&bf)[KT], const f32x16& c_init = f32x16{}) {
   static_assert(PF <= KT, "bad chain shape");
-  f32x16 c = f32x16{};
+  f32x16 c = c_init;
   i16x8 a[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, koff[i & 7] + 256 * (i >> 3) + extra);
@@ -326,10 +326,10 @@ __device__ __forceinline__ int kstep_off(int base, int kk) { return (base ^ ((kk
 // mma_chain1_lds with the k-step offsets derived from one base (kstep_off).
 template <bool IS_BF16, int KT, int PF, int SG = 0>
 __device__ __forceinline__ f32x16 mma_chain1_lds_b(const char GFA_LDS* tile, int koff0, int extra,
-                                                   const i16x8 (&bf)[KT]) {
+                                                   const i16x8 (&bf)[KT], const f32x16& c_init = f32x16{}) {
   static_assert(PF <= KT, "bad chain shape");
   const int kb = opaque(koff0) + extra;
-  f32x16 c = f32x16{};
+  f32x16 c = c_init;
   i16x8 a[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, kstep_off(kb, i));
@@ -354,11 +354,11 @@ __device__ __forceinline__ f32x16 mma_chain1_lds_b(const char GFA_LDS* tile, int
 // mma_chain1_lds_b with NL tile-copy instructions spread over the chain (as mma_chain1_lds_ld).
 template <bool IS_BF16, int KT, int PF, int NL, typename LD>
 __device__ __forceinline__ f32x16 mma_chain1_lds_ld_b(const char GFA_LDS* tile, int koff0, int extra,
-                                                      const i16x8 (&bf)[KT], LD&& ld) {
+                                                      const i16x8 (&bf)[KT], LD&& ld, const f32x16& c_init = f32x16{}) {
   static_assert(PF <= KT && NL >= 1 && KT % NL == 0, "bad chain shape");
   constexpr int EV = KT / NL;
   const int kb = opaque(koff0) + extra;
-  f32x16 c = f32x16{};
+  f32x16 c = c_init;
   i16x8 a[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, kstep_off(kb, i));

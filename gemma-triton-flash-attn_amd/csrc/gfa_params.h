@@ -78,6 +78,7 @@ struct BwdDkvParams {
   int B, Hq, Hkv, N, R;
   int causal, window;
   float scale, scale_log2;
+  float inv_scale;   // 1 / scale
   int q_splits;
   int lse_ld;
   int n_kb;          // number of key blocks (each WKV keys wide)

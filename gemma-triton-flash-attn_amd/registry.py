@@ -7,8 +7,9 @@ same role is one explicit table. Each entry names the tiles of the three gfx950 
 the forward runs one wave per 32 query rows over the full head dim, the dQ kernel
 ``dq_split`` waves per 32 query rows (a pair splitting the head dim at D=512, one wave at
 D <= 256), the dK/dV kernel ``dkv_roles`` waves per 32 keys (a role-split pair at D=512 and
-D=128, one wave doing all four products at D=256 and D=64). D=64 and D=128 cover the rest of the
-reference's documented head-dim range (64-512, powers of two; docs/api.md:63).
+D=128, one wave doing all four products at D=256 and D=64; with a sliding window D=256 runs
+role-split pairs at two waves per SIMD, the ``dkv_window`` form). D=64 and D=128 cover the rest
+of the reference's documented head-dim range (64-512, powers of two; docs/api.md:63).
 
 The C library holds the same table (csrc/gfa_api.hip, kRegistry); ``gfa_config`` reports
 what the library will use and the tests assert the two agree.
@@ -34,6 +35,15 @@ class KernelConfig:
     dkv_wgs_per_cu: int = 1  # dKV workgroups resident per CU (waves per SIMD)
     fwd_block_kv_options: tuple = ()  # other built forward tile widths (BLOCK_KV override)
     fwd_block_kv_window: int = 0      # forward tile with a sliding window (0 = fwd_block_kv)
+    # dK/dV form with a sliding window shorter than the sequence, (waves, roles, wgs_per_cu);
+    # () = the same as without one
+    dkv_window: tuple = ()
+
+    def dkv_form(self, windowed: bool) -> tuple:
+        """(waves, roles, workgroups per CU) of the dK/dV kernel."""
+        if windowed and self.dkv_window:
+            return self.dkv_window
+        return (self.dkv_waves, self.dkv_roles, self.dkv_wgs_per_cu)
 
 
 REGISTRY: dict[int, KernelConfig] = {
@@ -41,7 +51,7 @@ REGISTRY: dict[int, KernelConfig] = {
                       dkv_waves=4, dkv_roles=2,
                       fwd_block_kv_options=(32,)),
     256: KernelConfig(256, fwd_block_kv=32, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
-                      dkv_waves=4, dkv_roles=1,
+                      dkv_waves=4, dkv_roles=1, dkv_window=(4, 2, 2),
                       fwd_block_kv_options=(32, 64)),
     128: KernelConfig(128, fwd_block_kv=64, fwd_waves=4, dq_block_kv=32, dq_waves=4, dq_split=1, dkv_block_q=32,
                       dkv_waves=4, dkv_roles=2,
@@ -109,8 +119,8 @@ def q_splits_for_problem(batch: int, heads_kv: int, seq_len: int, head_dim: int,
     """The split count gfa_bwd uses (q_splits = 0) for one problem."""
     c = lookup(head_dim)
     windowed = causal and 0 < window < seq_len
-    return q_splits_for(batch, heads_kv, seq_len, c.dkv_waves // c.dkv_roles, c.dkv_wgs_per_cu,
-                        causal and not windowed)
+    waves, roles, wgs = c.dkv_form(windowed)
+    return q_splits_for(batch, heads_kv, seq_len, waves // roles, wgs, causal and not windowed)
 
 
 def get_config(batch: int, heads_q: int, heads_kv: int, seq_len: int, head_dim: int) -> dict:

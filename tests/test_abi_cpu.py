@@ -72,6 +72,20 @@ def test_config_matches_python_registry(shape):
     assert _lib.config(*shape) == gfa.get_config(*shape)
 
 
+@pytest.mark.parametrize("D", [64, 128, 256, 512])
+@pytest.mark.parametrize("B,Hkv,N", [(1, 8, 16384), (1, 1, 16384), (1, 8, 4096), (2, 2, 8192), (1, 1, 1024)])
+@pytest.mark.parametrize("causal,window", [(True, 0), (True, 512), (True, 1024), (True, 1 << 20), (False, 0),
+                                           (False, 512)])
+def test_query_split_choice_matches_python_registry(D, B, Hkv, N, causal, window):
+    """The library's split count (seen through the workspace it asks for) is the Python
+    registry's, windowed dK/dV form included."""
+    from gemma_triton_flash_attn_amd.registry import q_splits_for_problem
+
+    qs = q_splits_for_problem(B, Hkv, N, D, causal, window)
+    want = 0 if qs == 1 else qs * 2 * B * Hkv * N * D * 4
+    assert _lib.bwd_workspace_size(B, 2 * Hkv, Hkv, N, D, causal, window) == want
+
+
 def _fwd_args(**over):
     a = _lib.FwdArgs()
     a.q = a.k = a.v = a.o = 256  # fake, 16-byte aligned: validation happens before any launch

@@ -150,16 +150,18 @@ def test_deterministic(device):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("qs,D", [(2, 256), (4, 256), (8, 256), (2, 512), (8, 512), (4, 128), (8, 64)])
-def test_q_splits_match(qs, D, device):
-    """Q-split fp32 partials + reduction agree with the single-split kernel (both dK/dV
-    kernel forms: one wave per 32 keys at D <= 256, role-split pairs at D=512)."""
+@pytest.mark.parametrize("qs,D,window", [(2, 256, 0), (4, 256, 0), (8, 256, 0), (2, 256, 64), (8, 256, 100),
+                                          (2, 512, 0), (8, 512, 0), (4, 128, 0), (8, 64, 0)])
+def test_q_splits_match(qs, D, window, device):
+    """Q-split fp32 partials + reduction agree with the single-split kernel (every dK/dV
+    kernel form: one wave per 32 keys at D=256 and D=64, role-split pairs at D=512 and D=128,
+    and at D=256 with a window)."""
     from gemma_triton_flash_attn_amd.attention import _backward, _forward
 
     q, k, v, do = make_inputs(1, 8, 1, 256, D, torch.bfloat16, device, seed=5)
-    o, lse = _forward(q, k, v, True, 0, D ** -0.5, store_lse=True)
-    ref = _backward(q, k, v, o, lse, do, True, 0, D ** -0.5, q_splits=1)
-    got = _backward(q, k, v, o, lse, do, True, 0, D ** -0.5, q_splits=qs)
+    o, lse = _forward(q, k, v, True, window, D ** -0.5, store_lse=True)
+    ref = _backward(q, k, v, o, lse, do, True, window, D ** -0.5, q_splits=1)
+    got = _backward(q, k, v, o, lse, do, True, window, D ** -0.5, q_splits=qs)
     torch.cuda.synchronize()
     assert torch.equal(ref[0], got[0])  # dQ does not depend on the split
     for a, b in zip(ref[1:3], got[1:3]):
