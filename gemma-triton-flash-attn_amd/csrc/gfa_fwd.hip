@@ -103,6 +103,20 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   // the workgroup's keys, which is fully masked (and zero-filled past the sequence end).
   // An empty range (k_hi <= k_lo, only with segments) gives no tiles at all.
   const int t_hi = t_lo + ((((k_hi + BKV - 1) / BKV) - t_lo + 1) & ~1);
+  // Sliding window at D=256: the loop's tile t reads tile rot(t), a cyclic walk of [t_lo, t_hi)
+  // that starts at the tile whose index is a multiple of the tile count, so that step j of
+  // every workgroup reads a tile with index = j (mod count). The neighbouring query blocks that
+  // run together on one XCD then read the same K / V tiles at the same time and share them in
+  // L2 (each started at its own first tile, they run a few tiles apart): 1-3.5% faster on
+  // windows of 512 and 1024. Other head dims walk in order: at D=512 the extra scalar state
+  // spills (1-2% slower), at D=128 it is even.
+  constexpr bool ROT = D == 256;
+  const int nt = t_hi - t_lo;
+  const int t_shift = (ROT && swa && nt > 0) ? (nt - t_lo % nt) % nt : 0;
+  auto rot = [&](int t) __attribute__((always_inline)) {
+    if constexpr (!ROT) return t;
+    return t + t_shift < t_hi ? t + t_shift : t + t_shift - nt;
+  };
 
   // Keys every query of this wave sees: [all_lo, all_hi).
   const bool active = q0 < p.N;
@@ -168,8 +182,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     __builtin_amdgcn_s_setprio(1);
     // The last step re-fetches its own tile into the idle buffers (never read) so the
     // body stays branch-free.
-    const int rn = min(t + 1, t_hi - 1) * BKV;
-    const int k0 = t * BKV;
+    const int rn = rot(min(t + 1, t_hi - 1)) * BKV;
+    const int k0 = rot(t) * BKV;
     f32x16 s[SB];
     s[0] = mma_chain1_lds_ld_b<IS_BF16, KT, PF, 2 * NI>(kt, koff0, 0, qf, [&](int i) {
       if (i < NI) {
@@ -246,8 +260,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
     l_run = 0.f;
     if (t_lo < t_hi) {
-      kload.load(t_lo * BKV, K0);
-      vload.load(t_lo * BKV, V0);
+      kload.load(rot(t_lo) * BKV, K0);
+      vload.load(rot(t_lo) * BKV, V0);
     }
     for (int t = t_lo; t < t_hi; t += 2) {
       // Scheduling fences keep the two tile steps from being interleaved, which would

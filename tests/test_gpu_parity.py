@@ -168,11 +168,12 @@ def test_q_splits_match(qs, D, window, device):
         assert _rel(_np(b), _np(a)) < 1e-2
 
 
-@pytest.mark.parametrize("dtype,jump,D", [(torch.float16, 16.0, 256), (torch.bfloat16, 60.0, 256),
-                                         (torch.float16, 5.0, 256), (torch.float16, 16.0, 128),
-                                         (torch.float16, 16.0, 64), (torch.float16, 16.0, 512),
-                                         (torch.bfloat16, 60.0, 512)])
-def test_late_large_scores(dtype, jump, D, device):
+@pytest.mark.parametrize("dtype,jump,D,window", [(torch.float16, 16.0, 256, 0), (torch.bfloat16, 60.0, 256, 0),
+                                                (torch.float16, 5.0, 256, 0), (torch.float16, 16.0, 128, 0),
+                                                (torch.float16, 16.0, 64, 0), (torch.float16, 16.0, 512, 0),
+                                                (torch.bfloat16, 60.0, 512, 0), (torch.float16, 16.0, 256, 150),
+                                                (torch.float16, 16.0, 512, 150)])
+def test_late_large_scores(dtype, jump, D, window, device):
     """Scores that grow far above the first tile's maximum. The forward fixes each row's
     reference max at its first visible tile; rows whose later scores exceed it by more
     than the 16-bit-safe margin force the exact-max second pass. Both paths must agree
@@ -182,7 +183,7 @@ def test_late_large_scores(dtype, jump, D, device):
     one-hot and dS = P * (dP - delta) cancels, with delta = rowsum(dO * O) taken from the
     stored bf16 O (as in the reference, attention.py:733-742); the 2^-9 rounding of O then
     dominates dQ. For that case only the forward and the finiteness of the gradients are
-    checked."""
+    checked. With a window the D=256 forward walks its key tiles cyclically, not in order."""
     B, Hq, Hkv, N = 1, 4, 2, 192
     g = torch.Generator().manual_seed(9)
     q = torch.randn(B, Hq, N, D, generator=g) * 0.1
@@ -194,9 +195,9 @@ def test_late_large_scores(dtype, jump, D, device):
     q += u * 4.0
     k[:, :, 100:] += u * (jump * D ** 0.5 / 4.0)
     q, k, v, do = (t.to(device=device, dtype=dtype) for t in (q, k, v, do))
-    o, dq, dk, dv = _run(q, k, v, do, True, 0)
-    o_ref, _ = orc.forward(_np(q), _np(k), _np(v), True, 0)
-    dq_ref, dk_ref, dv_ref, _ = orc.backward(_np(q), _np(k), _np(v), _np(do), True, 0)
+    o, dq, dk, dv = _run(q, k, v, do, True, window)
+    o_ref, _ = orc.forward(_np(q), _np(k), _np(v), True, window)
+    dq_ref, dk_ref, dv_ref, _ = orc.backward(_np(q), _np(k), _np(v), _np(do), True, window)
     assert torch.isfinite(o).all()
     assert float(np.abs(_np(o) - o_ref).max()) <= O_TOL[dtype]
     for got, ref in ((dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
