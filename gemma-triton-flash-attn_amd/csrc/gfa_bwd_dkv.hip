@@ -60,6 +60,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
 
   constexpr bool STAGE = dkv_stages_rows(D, ROLES);
+  // Role pairs at two waves per SIMD (D=256): each wave stages its one stationary operand (K or
+  // V rows) and its one accumulator's output rows through its own tile buffer.
+  constexpr bool STAGE_PAIR = ROLES == 2 && D == 256 && WPE == 2;
+  static_assert(!STAGE_PAIR || NW == 4, "one tile buffer per wave");
 
   __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NU * PX];
   char GFA_LDS* smem = (char GFA_LDS*)smem_raw;
@@ -146,7 +150,20 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   int roff[8];  // tile rows (A operand of S / dP): row l32, chunk 2*kk + h  (+256 * (kk >> 3))
 #pragma unroll
   for (int kl = 0; kl < 8; ++kl) roff[kl] = l32 * (2 * D) + (((2 * kl + h) ^ swz<D>(l32)) << 4);
-  if constexpr (STAGE) {
+  if constexpr (STAGE_PAIR) {
+    // This role's rows (K or V) into tile buffer `wave` (idle before the loop) in whole-row
+    // copies, read back in the operand layout.
+    char GFA_LDS* blk = smem + wave * TILE;
+    if (role == 0) {
+      copy_rows_lds<D>(p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh, p.kv.sn, p.N, k0, lane, blk);
+    } else {
+      copy_rows_lds<D>(p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh, p.vv.sn, p.N, k0, lane, blk);
+    }
+    drain_tile_copies();
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) sf[0][kk] = lds_read16(blk, roff[kk & 7] + 256 * (kk >> 3));
+    barrier_lds();  // every wave has read its rows out of the tile buffers
+  } else if constexpr (STAGE) {
     // K rows into tile buffer `wave` (idle before the loop), V rows into the stage block, in
     // whole-row copies; read back in the operand layout.
     static_assert(NS == 2 && NU == 4, "one wave per 32 keys, four per workgroup");
@@ -582,7 +599,35 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   drain_tile_copies();
 
   // ---- epilogue: lane = key, registers = head-dim rows 32*db + 8*g + 4*h + e ----
-  if (STAGE && p.q_splits == 1) {
+  if (STAGE_PAIR && p.q_splits == 1) {
+    // This wave's dV or dK rows through its tile buffer (after every wave is done with the last
+    // tiles), then whole rows to HBM. The lane index is made opaque so the addresses are
+    // computed here, not kept live over the loop from the prologue.
+    barrier_lds();
+    char GFA_LDS* sblk = smem + wave * TILE;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int r32 = ln & 31;
+    const int hh = ln >> 5;
+    const float osc = role == 0 ? 1.f : p.scale;  // dK carries the softmax scale
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        i16x4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[0][db][4 * g + e] * osc);
+        const int c = 4 * db + g;  // 16-byte chunk of row r32 that holds these 4 + 4 elements
+        *reinterpret_cast<i16x4 GFA_LDS*>(sblk + r32 * (2 * D) + ((c ^ swz<D>(r32)) << 4) + 8 * hh) = o4;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (role == 0) {
+      store_rows_lds<D>(p.dv + (int64_t)b * p.dvv.sb + (int64_t)kvh * p.dvv.sh, p.dvv.sn, active ? p.N : 0, k0, ln, sblk);
+    } else {
+      store_rows_lds<D>(p.dk + (int64_t)b * p.dkv.sb + (int64_t)kvh * p.dkv.sh, p.dkv.sn, active ? p.N : 0, k0, ln, sblk);
+    }
+  } else if (STAGE && p.q_splits == 1) {
     // dV, then dK rows through this wave's stage block (idle since the prologue; laid out like
     // a tile), then whole rows to HBM. The lane index is made opaque here so the addresses are
     // computed here, not shared with the prologue's (which keeps them live over the loop).
