@@ -26,8 +26,10 @@
 //    tile in which a row sees a key sets m_ref, later tiles use p = exp2(s - m_ref), so the
 //    loop never rescales O. If any row later meets a score above m_ref + kMargin (P could
 //    leave the 16-bit range) the workgroup redoes its rows once with m_ref = the exact row
-//    max observed in the first pass. Exact either way (LSE = m_ref + log2 l); the second
-//    pass is never taken for ordinary inputs.
+//    max (observed in the first pass; for bf16 at D <= 256, where the first pass takes the
+//    tile max only until m_ref is set and judges overflow from the row sum, found by a pass
+//    that runs the score chains alone). Exact either way (LSE = m_ref + log2 l); the redo
+//    is never taken for ordinary inputs.
 //  * Scores are scaled by scale*log2(e) once and exponentiated with v_exp_f32. Causal and
 //    window masks are evaluated only on tiles that straddle a boundary.
 #include "gfa_common.h"
@@ -45,6 +47,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   // Largest allowed exp2 argument: P stays below 2^15 in fp16 (max 65504); bf16 P and the
   // fp32 accumulators have range to spare.
   constexpr float kMargin = IS_BF16 ? 64.0f : 15.0f;
+  constexpr float kMaxRowSum = 18446744073709551616.0f;  // 2^64 = 2^kMargin for bf16
   static_assert(BKV % 32 == 0, "BKV must be a multiple of 32");
   static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
   // LDS read-ahead of the score chain: shallower when several waves share a SIMD's registers.
@@ -173,8 +176,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   // One key tile: wait for it, then S^T = K Q^T with the copy of tile t+1 into the other
   // buffers spread over the chain, softmax against the fixed reference max, O^T += V^T P^T.
   constexpr int NI = TileLoader<D, BKV, NW>::NI;  // copy instructions per tile and wave
-  auto step = [&](int t, const char GFA_LDS* kt, const char GFA_LDS* vt, char GFA_LDS* kn,
+  // bf16 at D <= 256 (LAZY): the tile's row max is taken only while some row of the wave has no
+  // reference max yet (a wave-uniform test), and overflow is judged once per pass from the row
+  // sum: a P above 2^kMargin makes l above it too. The rare redo then first finds the exact row
+  // max in a pass that runs the S^T chains alone (MODE 1). 6% faster at D=64, 3% at D=128, 1% at
+  // D=256; at D=512 (one wave per SIMD, the max hidden under the chain) 1% slower. fp16's margin
+  // (2^15) is within reach of a long row's sum, so fp16 keeps the per-tile max and check.
+  constexpr bool LAZY = IS_BF16 && D <= 256;
+  auto step = [&](auto mode, int t, const char GFA_LDS* kt, const char GFA_LDS* vt, char GFA_LDS* kn,
                   char GFA_LDS* vn) __attribute__((always_inline)) {
+    constexpr int MODE = decltype(mode)::value;  // 0: accumulate; 1: row max only
     barrier_tile();  // tile t landed; every wave is done reading the other buffers
     // Issue priority: raised while the wave runs MFMA chains, normal during the softmax, so
     // that with several waves on a SIMD the matrix unit is fed first and the waves drift
@@ -215,17 +226,28 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     // Row max of the scaled scores as scale * (max of the raw ones): the scale is positive
     // (checked at the boundary; masking to -inf before scaling needs that too), so one
     // multiply replaces sixteen. The exponent argument scales each score in its FMA.
-    float mt = -INFINITY;
+    auto row_max = [&]() __attribute__((always_inline)) {
+      float m = -INFINITY;
 #pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
+      for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sb][r]);
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, s[sb][r]);
+      }
+      return halves_max(m) * p.scale_log2;
+    };
+    if constexpr (MODE == 1) {
+      m_seen = fmaxf(m_seen, row_max());
+      return;
     }
-    mt = halves_max(mt) * p.scale_log2;
-    // First tile with a visible key fixes m_ref; acc and l are still zero for this row.
-    m_ref = (m_ref == kNegBig && mt > kNegBig) ? mt : m_ref;
-    ovf = ovf || (mt > m_ref + kMargin);
-    m_seen = fmaxf(m_seen, mt);
+    if (!LAZY || __builtin_amdgcn_ballot_w64(m_ref == kNegBig) != 0) {
+      const float mt = row_max();
+      // First tile with a visible key fixes m_ref; acc and l are still zero for this row.
+      m_ref = (m_ref == kNegBig && mt > kNegBig) ? mt : m_ref;
+      if constexpr (!LAZY) {
+        ovf = ovf || (mt > m_ref + kMargin);
+        m_seen = fmaxf(m_seen, mt);
+      }
+    }
     i16x8 pb[BKV / 16];
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
@@ -255,7 +277,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   // One pass over the workgroup's key tiles. Written once, expanded twice below: the
   // rare redo pass is a second straight-line copy rather than an outer loop, which keeps
   // the accumulators' live ranges simple enough to stay in AGPRs.
-  auto run_pass = [&]() __attribute__((always_inline)) {
+  auto run_pass = [&](auto mode) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
     l_run = 0.f;
@@ -266,19 +288,25 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     for (int t = t_lo; t < t_hi; t += 2) {
       // Scheduling fences keep the two tile steps from being interleaved, which would
       // raise register pressure past the VGPR budget.
-      step(t, K0, V0, K1, V1);
+      step(mode, t, K0, V0, K1, V1);
       __builtin_amdgcn_sched_barrier(0);
-      step(t + 1, K1, V1, K0, V0);
+      step(mode, t + 1, K1, V1, K0, V0);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  run_pass();
+  constexpr std::integral_constant<int, 0> kAccumulate{};
+  run_pass(kAccumulate);
+  if constexpr (LAZY) ovf = halves_sum(l_run) > kMaxRowSum;
   // Workgroup vote: does any row need the exact-max redo?
   if (__any(ovf) && lane == 0) redo_flag = 1;
   barrier_tile();  // also drains the last (redundant) prefetch before LDS is reused
   if (redo_flag != 0) {
+    if constexpr (LAZY) {
+      run_pass(std::integral_constant<int, 1>{});  // exact row max into m_seen
+      barrier_tile();
+    }
     m_ref = m_seen;
-    run_pass();
+    run_pass(kAccumulate);
     drain_tile_copies();  // the redo pass's last (redundant) prefetch, as after the first pass
   }
 

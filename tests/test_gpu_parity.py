@@ -172,7 +172,8 @@ def test_q_splits_match(qs, D, window, device):
                                                 (torch.float16, 5.0, 256, 0), (torch.float16, 16.0, 128, 0),
                                                 (torch.float16, 16.0, 64, 0), (torch.float16, 16.0, 512, 0),
                                                 (torch.bfloat16, 60.0, 512, 0), (torch.float16, 16.0, 256, 150),
-                                                (torch.float16, 16.0, 512, 150)])
+                                                (torch.float16, 16.0, 512, 150), (torch.bfloat16, 60.0, 128, 0),
+                                                (torch.bfloat16, 60.0, 256, 150), (torch.bfloat16, 40.0, 256, 0)])
 def test_late_large_scores(dtype, jump, D, window, device):
     """Scores that grow far above the first tile's maximum. The forward fixes each row's
     reference max at its first visible tile; rows whose later scores exceed it by more
@@ -183,7 +184,10 @@ def test_late_large_scores(dtype, jump, D, window, device):
     one-hot and dS = P * (dP - delta) cancels, with delta = rowsum(dO * O) taken from the
     stored bf16 O (as in the reference, attention.py:733-742); the 2^-9 rounding of O then
     dominates dQ. For that case only the forward and the finiteness of the gradients are
-    checked. With a window the D=256 forward walks its key tiles cyclically, not in order."""
+    checked. With a window the D=256 forward walks its key tiles cyclically, not in order. In
+    bf16 at D <= 256 the forward judges overflow from the row sum and finds the exact row max
+    for the redo in a pass of its own; a 40-nat gap (58 in log2) stays under the 2^64 margin and
+    is computed without a redo, with P up to 2^58."""
     B, Hq, Hkv, N = 1, 4, 2, 192
     g = torch.Generator().manual_seed(9)
     q = torch.randn(B, Hq, N, D, generator=g) * 0.1
@@ -195,11 +199,16 @@ def test_late_large_scores(dtype, jump, D, window, device):
     q += u * 4.0
     k[:, :, 100:] += u * (jump * D ** 0.5 / 4.0)
     q, k, v, do = (t.to(device=device, dtype=dtype) for t in (q, k, v, do))
+    from gemma_triton_flash_attn_amd.attention import _forward
+
     o, dq, dk, dv = _run(q, k, v, do, True, window)
-    o_ref, _ = orc.forward(_np(q), _np(k), _np(v), True, window)
+    o_ref, lse_ref = orc.forward(_np(q), _np(k), _np(v), True, window)
     dq_ref, dk_ref, dv_ref, _ = orc.backward(_np(q), _np(k), _np(v), _np(do), True, window)
     assert torch.isfinite(o).all()
     assert float(np.abs(_np(o) - o_ref).max()) <= O_TOL[dtype]
+    _, lse = _forward(q, k, v, True, window, D ** -0.5, store_lse=True)
+    lse = _np(lse)[..., :N]
+    assert float((np.abs(lse - lse_ref) / np.maximum(1.0, np.abs(lse_ref))).max()) <= 1e-3
     for got, ref in ((dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
         assert torch.isfinite(got).all()
         if dtype == torch.float16:
