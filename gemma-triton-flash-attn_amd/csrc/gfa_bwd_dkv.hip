@@ -205,7 +205,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // Role pairs at two waves per SIMD and D=256 (register-bound): the score chains start from
   // the row statistic instead of zero, so neither LSE nor delta stays live past the chain:
   // role 0 from -LSE / scale (P = exp2(scale * log2e * acc)), role 1 from -delta (dS = P acc).
-  constexpr bool INIT = ROLES == 2 && !SHARED && D == 256;
+  constexpr bool INIT = ROLES == 2 && D == 256;
   const int roff0 = l32 * (2 * D) + ((h ^ swz<D>(l32)) << 4);  // tile row l32, chunk h (k-step 0)
   int toff0;  // tiles read transposed (A operands of dV^T, dK^T): rows 4h + t/4, column block 0
   int toffA[4], toffB[4];
@@ -387,15 +387,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
         }
       }
       __builtin_amdgcn_sched_barrier(0);
+      i16x8 pb_sh[BQ / 16];  // shared form: P (role 0) or dS (role 1), packed, both halves
       if constexpr (SHARED) {
         // Shared softmax: role RO turns the rows of registers 8 RO .. 8 RO + 7 (g = 2 RO,
         // 2 RO + 1) into P and dS. Each role first hands its partner the half of its own chain
         // result the partner needs (role 0: S of registers 8..15; role 1: dP of 0..7), then
-        // each hands back the half the partner accumulates (role 1: P of 8..15 for dV; role 0:
-        // dS of 0..7 for dK). Exchange slots of one score block: 0 S half, 1 dP half, 2 P
-        // half, 3 dS half (two 1 KB planes of f32x4 each). Split this way neither wave waits
-        // for the other's exponentials or dS; with P computed by role 0 alone, role 1 sat out
-        // about 20% of each step.
+        // each hands back, packed to 16 bits, the half the partner accumulates (role 1: P of
+        // 8..15 for dV; role 0: dS of 0..7 for dK). Exchange slots of one score block: 0 S half,
+        // 1 dP half (two 1 KB planes of f32x4 each), 2 P half, 3 dS half (one 1 KB plane of
+        // i16x8 each). Split this way neither wave waits for the other's exponentials or dS;
+        // with P computed by role 0 alone, role 1 sat out about 20% of each step.
         const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
         auto slot = [&](int sb, int k, int j) __attribute__((always_inline)) { return pxr + (sb * 4 + k) * 2048 + j * 1024; };
         auto shared = [&](auto ro) __attribute__((always_inline)) {
@@ -410,7 +411,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
             }
           }
           barrier_lds();  // both halves of both chains are in the slots
-          float mine[SB][8];  // role 0: P of its half; role 1: dS of its half
   #pragma unroll
           for (int sb = 0; sb < SB; ++sb) {
             f32x4 w[2];
@@ -434,28 +434,21 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
               const float dpv = RO == 1 ? s[sb][MH + i] : w[i >> 2][i & 3];
               dsv[i] = pv[i] * (dpv - st[0][sb][2 + (i >> 2)][i & 3]);
             }
-            // hand back what the partner accumulates: role 0 its dS half, role 1 its P half
+            // Packed to 16 bits (the accumulations' B operand): the half this role accumulates
+            // stays, the half the partner accumulates goes to its slot (role 0: dS, role 1: P).
+            i16x8 keep, give;
   #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const f32x4 v = RO == 0 ? f32x4{dsv[4 * j], dsv[4 * j + 1], dsv[4 * j + 2], dsv[4 * j + 3]}
-                                      : f32x4{pv[4 * j], pv[4 * j + 1], pv[4 * j + 2], pv[4 * j + 3]};
-              *reinterpret_cast<f32x4 GFA_LDS*>(slot(sb, RO == 0 ? 3 : 2, j)) = v;
+            for (int i = 0; i < 8; ++i) {
+              keep[i] = to16<IS_BF16>(RO == 0 ? pv[i] : dsv[i]);
+              give[i] = to16<IS_BF16>(RO == 0 ? dsv[i] : pv[i]);
             }
-  #pragma unroll
-            for (int i = 0; i < 8; ++i) mine[sb][i] = RO == 0 ? pv[i] : dsv[i];
+            *reinterpret_cast<i16x8 GFA_LDS*>(slot(sb, RO == 0 ? 3 : 2, 0)) = give;
+            pb_sh[sb * 2 + RO] = keep;
           }
           barrier_lds();  // the halves handed back are in the slots
   #pragma unroll
-          for (int sb = 0; sb < SB; ++sb) {
-  #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const f32x4 w = *reinterpret_cast<const f32x4 GFA_LDS*>(slot(sb, RO == 0 ? 2 : 3, j));
-  #pragma unroll
-              for (int e = 0; e < 4; ++e) s[sb][OH + 4 * j + e] = w[e];
-            }
-  #pragma unroll
-            for (int i = 0; i < 8; ++i) s[sb][MH + i] = mine[sb][i];
-          }
+          for (int sb = 0; sb < SB; ++sb)
+            pb_sh[sb * 2 + 1 - RO] = *reinterpret_cast<const i16x8 GFA_LDS*>(slot(sb, RO == 0 ? 2 : 3, 0));
         };
         if (role == 0) {
           shared(std::integral_constant<int, 0>{});
@@ -495,9 +488,14 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
           }
         }
       }
-      // s now holds P (role 0) or dS (role 1) for all 32 queries.
+      // s now holds P (role 0) or dS (role 1) for all 32 queries (shared form: pb_sh, packed).
       i16x8 pb[BQ / 16];
-      pack(s, pb);
+      if constexpr (SHARED) {
+#pragma unroll
+        for (int i = 0; i < BQ / 16; ++i) pb[i] = pb_sh[i];
+      } else {
+        pack(s, pb);
+      }
       __builtin_amdgcn_sched_barrier(0);
       accumulate(acc[0], tt, pb);
       __builtin_amdgcn_sched_barrier(0);
@@ -558,6 +556,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     // multiple of 64), issued before the prefetch so they are not queued behind it.
     f32x4 st[NS][SB][4];
     if constexpr (SHARED) {
+      // each role's half of the rows (registers 8 role .. 8 role + 7): LSE, then delta
       const int64_t roff = (int64_t)r_c * p.lse_ld + q0 + 4 * h + 16 * role;
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb)
@@ -566,17 +565,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
           st[0][sb][j] = *reinterpret_cast<const f32x4*>(stat_kv0 + roff + sb * 32 + 8 * j);
           st[0][sb][2 + j] = *reinterpret_cast<const f32x4*>(stat_kv1 + roff + sb * 32 + 8 * j);
         }
-    } else {
+    } else
 #pragma unroll
-      for (int i = 0; i < NS; ++i) {
-        // pair (hand-off form): LSE for role 0, delta for role 1
-        const float* sbase = (ROLES == 2 && role == 1) || i == 1 ? stat_kv1 : stat_kv0;
-        const float* srow = sbase + (int64_t)r_c * p.lse_ld + q0 + 4 * h;
+    for (int i = 0; i < NS; ++i) {
+      // pair: LSE for role 0, delta for role 1 (the start of its chain)
+      const float* sbase = (ROLES == 2 && role == 1) || i == 1 ? stat_kv1 : stat_kv0;
+      const float* srow = sbase + (int64_t)r_c * p.lse_ld + q0 + 4 * h;
 #pragma unroll
-        for (int sb = 0; sb < SB; ++sb)
+      for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) st[i][sb][g] = *reinterpret_cast<const f32x4*>(srow + sb * 32 + 8 * g);
-      }
+        for (int g = 0; g < 4; ++g) st[i][sb][g] = *reinterpret_cast<const f32x4*>(srow + sb * 32 + 8 * g);
     }
     // Next tile; the last iteration re-fetches its own tile into the idle buffer (never
     // read) so the loop body stays branch-free.
