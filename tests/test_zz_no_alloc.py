@@ -51,7 +51,10 @@ def _noalloc_splits(B, Hq, Hkv, N, D, causal, window):
     from gemma_triton_flash_attn_amd.attention import lse_ld
 
     delta = (B * Hq * lse_ld(N) * 4 + 255) // 256 * 256
-    qs = _lib.config(B, Hq, Hkv, N, D)["q_splits"]
+    # the registry's count for this mask (a window has its own dK/dV form), seen through the
+    # workspace gfa_bwd asks for
+    ws = _lib.bwd_workspace_size(B, Hq, Hkv, N, D, causal, window, 0)
+    qs = ws // (2 * B * Hkv * N * D * 4) if ws else 1
     while qs > 1 and delta + _lib.bwd_workspace_size(B, Hq, Hkv, N, D, causal, window, qs) > _lib.NOALLOC_SCRATCH_BYTES:
         qs //= 2
     return qs
