@@ -165,8 +165,11 @@ int gfa_bwd_noalloc(const gfa_bwd_args* args);
 size_t gfa_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len, int32_t head_dim,
                               int32_t causal, int32_t window, int32_t q_splits);
 
-/* Fill *out with the configuration used for this problem without a sliding window (a
- * windowed forward at head_dim 128 runs 32-key tiles instead). Returns a gfa_status. */
+/* Fill *out with the configuration used for this problem without a sliding window (with a
+ * window shorter than the sequence, the forward at head_dim 128 runs 32-key tiles, and the
+ * dK/dV kernel at head_dim 256 runs role-split wave pairs, 64 keys per workgroup, two
+ * workgroups per CU; gfa_bwd_workspace_size reports the split count for either). Returns a
+ * gfa_status. */
 int gfa_config(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len, int32_t head_dim,
                gfa_config_info* out);
 
