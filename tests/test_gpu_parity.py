@@ -260,3 +260,33 @@ def test_delta_scratch_garbage_does_not_leak(N, D, window, segs, device):
     # every delta row a 32-row tile covers is finite
     n32 = (N + 31) // 32 * 32
     assert torch.isfinite(bufs[3][:, :, :n32]).all()
+
+
+@pytest.mark.parametrize("N,D,causal,window", [(100, 512, True, 0), (77, 256, True, 0), (150, 256, True, 48),
+                                               (70, 256, False, 0), (131, 128, True, 37), (45, 64, False, 0),
+                                               (300, 64, True, 0)])
+def test_nan_past_sequence_end_does_not_leak(N, D, causal, window, device):
+    """Every kernel reads whole 32-row tiles, also past row N - 1 of a (batch, head) slice.
+    With q, k, v and dO held as views of buffers whose rows past N are NaN, the output, LSE
+    and gradients must equal those of contiguous copies bit for bit: rows past N must be
+    zero-filled by the buffer range check or clamped, never read as data."""
+    B, Hq, Hkv = 2, 4, 2
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, torch.bfloat16, device, seed=3 * N + D)
+
+    def padded(t):
+        buf = torch.full((t.shape[0], t.shape[1], N + 128, D), float("nan"), dtype=t.dtype, device=device)
+        buf[:, :, :N] = t
+        return buf[:, :, :N]
+
+    ref = _run(q, k, v, do, causal, window)
+    got = _run(padded(q), padded(k), padded(v), padded(do), causal, window)
+    for a, r in zip(got, ref):
+        assert torch.isfinite(a.float()).all()
+        assert torch.equal(a, r)
+    from gemma_triton_flash_attn_amd.attention import _forward
+    sc = D ** -0.5
+    o_r, lse_r = _forward(q, k, v, causal, window, sc, store_lse=True)
+    o_g, lse_g = _forward(padded(q), padded(k), padded(v), causal, window, sc, store_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_g, o_r)
+    assert torch.equal(lse_g[:, :, :N], lse_r[:, :, :N])
