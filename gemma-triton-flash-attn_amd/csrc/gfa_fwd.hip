@@ -307,14 +307,22 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     }
     m_ref = m_seen;
     run_pass(kAccumulate);
-    drain_tile_copies();  // the redo pass's last (redundant) prefetch, as after the first pass
+    barrier_tile();  // the redo pass's last (redundant) prefetch landed; every wave is done with LDS
   }
 
   // ---- epilogue: normalise, store O and LSE ----
+  // O goes out through LDS (each wave's 32 rows in one of the four idle tile buffers) so that
+  // every store instruction writes whole rows: 16 bytes per lane, RPI rows per instruction,
+  // instead of 8 bytes into each of 32 rows. The wave reads back only what it wrote itself.
+  // The lane index is made opaque so that these addresses are computed here, not shared with
+  // the loop's (which would keep them live from the prologue).
+  char GFA_LDS* const sblk = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;
+  static_assert(TILE >= 32 * D * 2, "a tile buffer holds a wave's 32 output rows");
+  const int ln = opaque(lane);
+  const int r32 = ln & 31;
   const float l_tot = halves_sum(l_run);
   if (active && q < p.N) {
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;  // a row that sees no key (empty segment): O = 0
-    uint16_t* orow = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh + (int64_t)q * p.ov.sn;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -322,13 +330,15 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
         i16x4 o4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[db][4 * g + e] * inv);
-        *reinterpret_cast<i16x4*>(orow + db * 32 + 8 * g + 4 * h) = o4;
+        const int c = 4 * db + g;  // 16-byte chunk of row l32 that holds these 4 + 4 elements
+        *reinterpret_cast<i16x4 GFA_LDS*>(sblk + r32 * (2 * D) + ((c ^ swz<D>(r32)) << 4) + 8 * (ln >> 5)) = o4;
       }
     }
     if (p.store_lse && h == 0) {
       p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + q] = (m_ref + __log2f(l_tot)) * kLn2;
     }
   }
+  if (active) store_rows_lds<D>(p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh, p.ov.sn, p.N, q0, ln, sblk);
 }
 
 // Explicit instantiations of every built variant (both the device code and the host
