@@ -63,6 +63,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // Role pairs at two waves per SIMD (D=256): each wave stages its one stationary operand (K or
   // V rows) and its one accumulator's output rows through its own tile buffer.
   constexpr bool STAGE_PAIR = ROLES == 2 && D == 256 && WPE == 2;
+  constexpr bool PRIO = WPE >= 2;
   static_assert(!STAGE_PAIR || NW == 4, "one tile buffer per wave");
 
   __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NU * PX];
@@ -372,6 +373,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
         }
       }
       __builtin_amdgcn_sched_barrier(0);  // the MFMA pipelines are scheduled on their own
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
         if (sb == 0) {
@@ -387,6 +389,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
         }
       }
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
       i16x8 pb_sh[BQ / 16];  // shared form: P (role 0) or dS (role 1), packed, both halves
       if constexpr (SHARED) {
         // Shared softmax: role RO turns the rows of registers 8 RO .. 8 RO + 7 (g = 2 RO,
@@ -497,12 +500,15 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
         pack(s, pb);
       }
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
       accumulate(acc[0], tt, pb);
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     } else {
       // S = Q K^T, dP = dO V^T, then dV^T += dO^T P and dK^T += Q^T dS.
       f32x16 s[SB], dp[SB];
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
         if (sb == 0) {
@@ -521,6 +527,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
         }
       }
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
       make_p(s, st[0], q0);
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
@@ -533,10 +540,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       pack(s, pb);
       pack(dp, dsb);
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
       accumulate(acc[0], dt, pb);
       __builtin_amdgcn_sched_barrier(0);
       accumulate(acc[NS - 1], qt, dsb);
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     }
     // D >= 256: the accumulators fill the AGPRs and stay there. At D=64 everything fits the
     // VGPRs of two waves per SIMD; unpinned, the MFMAs write VGPRs directly (12% faster).

@@ -46,6 +46,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   // The swizzle permutes 16-chunk groups, so a head-dim half must be whole groups.
   static_assert(SPLIT == 1 || DH % 128 == 0, "a head-dim split needs halves of 128 or more elements");
   constexpr bool STAGE = dq_stages_rows(D, SPLIT);
+  constexpr bool PRIO = D <= 128;  // several waves per SIMD
   static_assert(!STAGE || NW == 4, "each wave stages its Q rows in one of four tile buffers");
 
   // Four distinct LDS tile objects (not one array indexed by a buffer id): with the loop
@@ -390,8 +391,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     }
     }
     // dQ^T[half] += K^T[half] dS^T, A operand read transposed from the K tile.
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
     mma_tr_accumulate<IS_BF16, D, DBH, BKV / 16, 2, 1>(acc, kt, toffA, toffB, dsb);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int db = 0; db < DBH; ++db) pin_agpr(acc[db]);
   };
