@@ -24,6 +24,14 @@ gradient. Pinned by tests/test_oracle.py against torch SDPA with the equivalent 
 mask (rows with a visible key) and against the segment-free oracle run on every segment
 alone (padded and packed batches).
 
+Logit soft-capping (``softcap`` > 0; the reference lists it as unsupported, README.md:255-262,
+and its HF adapter raises for it, hf_integration.py:60-63): the scaled score z = scale q.k is
+replaced by softcap * tanh(z / softcap) before the mask and the softmax, as transformers'
+eager attention does (models/gemma2/modeling_gemma2.py, eager_attention_forward). In the
+backward, dS is multiplied by the derivative 1 - tanh^2(z / softcap) before dQ and dK.
+Pinned by tests/test_oracle.py against that transformers function (forward) and torch
+autograd through it in float64 (backward).
+
 Two implementations of the same equations:
   * ``forward`` / ``backward``: numpy float64, dense (N x N per head) - small cases and
     golden vectors;
@@ -70,7 +78,15 @@ def _default_scale(d: int, scale):
     return 1.0 / math.sqrt(d) if scale is None else float(scale)
 
 
-def forward(q, k, v, causal=False, window=0, scale=None, segments=None):
+def _capped(s, softcap):
+    """Scores after soft-capping and the derivative factor 1 - tanh^2 (1 without a cap)."""
+    if not softcap:
+        return s, None
+    t = np.tanh(s / softcap)
+    return softcap * t, 1.0 - t * t
+
+
+def forward(q, k, v, causal=False, window=0, scale=None, segments=None, softcap=0.0):
     """O (B, Hq, N, D) and natural-log LSE (B, Hq, N), float64."""
     q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
     B, Hq, N, D = q.shape
@@ -84,7 +100,7 @@ def forward(q, k, v, causal=False, window=0, scale=None, segments=None):
         seen = mask.any(axis=1)[:, None]
         for h in range(Hq):
             g = h * Hkv // Hq
-            s = sc * (q[b, h] @ k[b, g].T)
+            s, _ = _capped(sc * (q[b, h] @ k[b, g].T), softcap)
             s = np.where(mask, s, -np.inf)
             mx = np.where(seen, s.max(axis=1, keepdims=True), 0.0)
             p = np.where(mask, np.exp(s - mx), 0.0)
@@ -94,13 +110,13 @@ def forward(q, k, v, causal=False, window=0, scale=None, segments=None):
     return o, lse
 
 
-def backward(q, k, v, do, causal=False, window=0, scale=None, segments=None):
+def backward(q, k, v, do, causal=False, window=0, scale=None, segments=None, softcap=0.0):
     """dQ, dK, dV (float64) and delta = rowsum(dO * O) for the loss sum(O * dO)."""
     q, k, v, do = (np.asarray(x, dtype=np.float64) for x in (q, k, v, do))
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     sc = _default_scale(D, scale)
-    o, lse = forward(q, k, v, causal, window, scale, segments)
+    o, lse = forward(q, k, v, causal, window, scale, segments, softcap)
     base = allowed_mask(N, causal, window)
     dq = np.zeros_like(q)
     dk = np.zeros_like(k)
@@ -110,10 +126,12 @@ def backward(q, k, v, do, causal=False, window=0, scale=None, segments=None):
         mask = _row_mask(base, segments, b)
         for h in range(Hq):
             g = h * Hkv // Hq
-            s = sc * (q[b, h] @ k[b, g].T)
+            s, dcap = _capped(sc * (q[b, h] @ k[b, g].T), softcap)
             p = np.where(mask, np.exp(np.where(mask, s - lse[b, h][:, None], 0.0)), 0.0)
             dp = do[b, h] @ v[b, g].T
             ds = p * (dp - delta[b, h][:, None])
+            if dcap is not None:
+                ds = ds * dcap
             dq[b, h] = sc * (ds @ k[b, g])
             dk[b, g] += sc * (ds.T @ q[b, h])
             dv[b, g] += p.T @ do[b, h]
@@ -139,7 +157,7 @@ def _chunk_mask(torch, q_lo, q_hi, n, causal, window, device, segments=None, b=0
     return m
 
 
-def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024, segments=None):
+def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024, segments=None, softcap=0.0):
     """torch fp32 O and LSE for (B, H, N, D) tensors of any float dtype / device.
     ``segments``: (lo, hi) integer tensors (B, N), as in ``forward``."""
     import torch
@@ -159,6 +177,8 @@ def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024, seg
                 for lo in range(0, N, chunk):
                     hi = min(N, lo + chunk)
                     s = (qf[lo:hi] @ kt) * sc
+                    if softcap:
+                        s = softcap * torch.tanh(s / softcap)
                     mask = _chunk_mask(torch, lo, hi, N, causal, window, q.device, segments, b)
                     seen = mask.any(dim=1, keepdim=True)
                     s = s.masked_fill(~mask, float("-inf"))
@@ -172,7 +192,7 @@ def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024, seg
 
 
 def backward_chunked(q, k, v, do, causal=False, window=0, scale=None, chunk=1024, o=None, lse=None,
-                     segments=None):
+                     segments=None, softcap=0.0):
     """torch fp32 dQ, dK, dV, delta. ``o``/``lse`` may be passed to skip the recomputation."""
     import torch
 
@@ -180,7 +200,7 @@ def backward_chunked(q, k, v, do, causal=False, window=0, scale=None, chunk=1024
     Hkv = k.shape[1]
     sc = _default_scale(D, scale)
     if o is None or lse is None:
-        o, lse = forward_chunked(q, k, v, causal, window, scale, chunk, segments)
+        o, lse = forward_chunked(q, k, v, causal, window, scale, chunk, segments, softcap)
     dq = torch.empty((B, Hq, N, D), dtype=torch.float32, device=q.device)
     dk = torch.zeros((B, Hkv, N, D), dtype=torch.float32, device=q.device)
     dv = torch.zeros((B, Hkv, N, D), dtype=torch.float32, device=q.device)
@@ -198,9 +218,14 @@ def backward_chunked(q, k, v, do, causal=False, window=0, scale=None, chunk=1024
                     hi = min(N, lo + chunk)
                     mask = _chunk_mask(torch, lo, hi, N, causal, window, q.device, segments, b)
                     s = (qf[lo:hi] @ kt) * sc
+                    t = torch.tanh(s / softcap) if softcap else None
+                    if softcap:
+                        s = softcap * t
                     p = torch.exp((s - lse[b, h, lo:hi, None].float()).masked_fill(~mask, 0.0)).masked_fill(~mask, 0.0)
                     dp = dof[lo:hi] @ vt
                     ds = p * (dp - delta[b, h, lo:hi, None])
+                    if softcap:
+                        ds = ds * (1.0 - t * t)
                     dq[b, h, lo:hi] = (ds @ kf) * sc
                     dk[b, g] += (ds.t().contiguous() @ qf[lo:hi]) * sc
                     dv[b, g] += p.t().contiguous() @ dof[lo:hi]

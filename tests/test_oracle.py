@@ -203,3 +203,59 @@ def test_cpu_baseline_restatement_matches_oracle(causal, window):
     ref, _ = orc.forward(q, k, v, causal, window)
     assert got.shape == ref.shape
     assert float(np.abs(got.double().numpy() - ref).max()) < 2e-5
+
+
+def _hf_eager64(q, k, v, do, causal, window, softcap):
+    """transformers' eager attention (the Gemma-2 implementation, which soft-caps the scaled
+    scores before the mask) in float64, with torch autograd for the gradients."""
+    from types import SimpleNamespace
+
+    from transformers.models.gemma2.modeling_gemma2 import eager_attention_forward
+
+    q, k, v = (torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in (q, k, v))
+    n, d = q.shape[2], q.shape[3]
+    mask = torch.tensor(orc.allowed_mask(n, causal, window))
+    add = torch.zeros(n, n, dtype=torch.float64).masked_fill(~mask, float("-inf"))[None, None]
+    module = SimpleNamespace(num_key_value_groups=q.shape[1] // k.shape[1], training=False, head_dim=d)
+    o, _ = eager_attention_forward(module, q, k, v, add, dropout=0.0, scaling=d ** -0.5, softcap=softcap)
+    o = o.transpose(1, 2)  # the function returns (B, N, H, D)
+    (o * torch.tensor(do)).sum().backward()
+    return o.detach().numpy(), q.grad.numpy(), k.grad.numpy(), v.grad.numpy()
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,causal,window,cap", [
+    (1, 4, 2, 13, 8, True, 0, 5.0), (2, 6, 2, 17, 8, True, 5, 2.0), (1, 2, 2, 9, 4, False, 0, 0.7),
+    (1, 8, 1, 11, 16, True, 64, 30.0)])
+def test_softcap_matches_transformers_eager(B, Hq, Hkv, N, D, causal, window, cap):
+    """Soft-capped scores (not in the reference; transformers' Gemma-2 eager attention is the
+    independent implementation): forward and float64 autograd gradients. Scores are scaled up
+    so that the cap bends them (a dropped tanh or a missing 1 - tanh^2 factor fails)."""
+    q, k, v, do = (_rand(s, 60 + i) * (3.0 if i < 2 else 1.0)
+                   for i, s in enumerate([(B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D), (B, Hq, N, D)]))
+    o_ref, dq_ref, dk_ref, dv_ref = _hf_eager64(q, k, v, do, causal, window, cap)
+    o, _ = orc.forward(q, k, v, causal, window, softcap=cap)
+    dq, dk, dv, _ = orc.backward(q, k, v, do, causal, window, softcap=cap)
+    # transformers runs its softmax in float32 whatever the input dtype: float32-level agreement
+    for a, r in ((o, o_ref), (dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
+        np.testing.assert_allclose(a, r, atol=2e-6, rtol=1e-4)
+    # the cap changes the result at these score magnitudes (the check above is not vacuous)
+    o_nocap, _ = orc.forward(q, k, v, causal, window)
+    assert float(np.abs(o_nocap - o).max()) > 1e-3
+
+
+def test_softcap_chunked_matches_dense_and_large_cap_is_no_cap():
+    B, Hq, Hkv, N, D = 1, 4, 2, 37, 8
+    q, k, v, do = (_rand(s, 80 + i) * (3.0 if i < 2 else 1.0)
+                   for i, s in enumerate([(B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D), (B, Hq, N, D)]))
+    for causal, window in ((True, 0), (True, 6), (False, 0)):
+        o, lse = orc.forward(q, k, v, causal, window, softcap=4.0)
+        dq, dk, dv, delta = orc.backward(q, k, v, do, causal, window, softcap=4.0)
+        tq, tk, tv, tdo = (torch.tensor(x, dtype=torch.float32) for x in (q, k, v, do))
+        o2, lse2 = orc.forward_chunked(tq, tk, tv, causal, window, chunk=8, softcap=4.0)
+        dq2, dk2, dv2, delta2 = orc.backward_chunked(tq, tk, tv, tdo, causal, window, chunk=8, softcap=4.0)
+        for a, b in ((o, o2), (lse, lse2), (dq, dq2), (dk, dk2), (dv, dv2), (delta, delta2)):
+            np.testing.assert_allclose(b.numpy(), a, atol=5e-5, rtol=1e-4)
+    # tanh(z / c) * c -> z as c grows
+    o_big, _ = orc.forward(q, k, v, True, 0, softcap=1e7)
+    o_none, _ = orc.forward(q, k, v, True, 0)
+    np.testing.assert_allclose(o_big, o_none, atol=1e-9)
