@@ -122,8 +122,18 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def _check_softcap(softcap) -> float:
+    """0.0 for no soft-capping; otherwise a finite positive float (transformers' ``softcap``)."""
+    if softcap is None:
+        return 0.0
+    c = float(softcap)
+    if not math.isfinite(c) or c < 0.0:
+        raise ValueError(f"softcap={softcap} must be finite and positive (None or 0 = off)")
+    return c
+
+
 def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bool, block_kv: int = 0,
-             segments=None):
+             segments=None, softcap: float = 0.0):
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     q, k, v = _prep(q), _prep(k), _prep(v)
@@ -143,6 +153,7 @@ def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bo
     a.dtype = _DTYPES[q.dtype]
     a.block_kv = int(block_kv)
     a.lse_ld = ld
+    a.softcap = float(softcap)
     a.stream = _stream(q.device)
     if segments is not None:
         a.seg_lo, a.seg_hi = segments[0].data_ptr(), segments[1].data_ptr()
@@ -152,7 +163,7 @@ def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bo
 
 
 def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, q_splits: int = 0,
-              stages: int = 0, out=None, noalloc: bool = False, segments=None):
+              stages: int = 0, out=None, noalloc: bool = False, segments=None, softcap: float = 0.0):
     """Run gfa_bwd. ``stages`` selects kernels (0 = all; GFA_BWD_DQ / GFA_BWD_DKV bits);
     ``out`` = (dq, dk, dv, delta) reuses caller buffers (profiling a single stage).
     ``noalloc`` calls gfa_bwd_noalloc instead: delta and the workspace then live in the
@@ -191,6 +202,7 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
     a.stages = int(stages)
     a.workspace = ws.data_ptr() if ws is not None else None
     a.workspace_bytes = ws_bytes
+    a.softcap = float(softcap)
     a.stream = _stream(q.device)
     if segments is not None:
         a.seg_lo, a.seg_hi = segments[0].data_ptr(), segments[1].data_ptr()
@@ -206,18 +218,19 @@ def _default_scale(d: int, scale: float | None) -> float:
 class FlashAttnGQAFunction(torch.autograd.Function):
     """Autograd function of the GQA flash attention (reference attention.py:1433-1622).
 
-    forward(q, k, v, causal, slide_size, scale=None, segments=None) -> O; saves q, k, v, O,
-    the fp32 LSE and the segment tables. backward(dO) -> dQ, dK, dV via gfa_bwd (dQ kernel
-    with fused delta, then pack-GQA dKV).
+    forward(q, k, v, causal, slide_size, scale=None, segments=None, softcap=None) -> O; saves
+    q, k, v, O, the fp32 LSE and the segment tables. backward(dO) -> dQ, dK, dV via gfa_bwd (dQ
+    kernel with fused delta, then pack-GQA dKV).
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, causal=False, slide_size=0, scale=None, segments=None):
+    def forward(ctx, q, k, v, causal=False, slide_size=0, scale=None, segments=None, softcap=None):
         _check_inputs(q, k, v)
         segments = _check_segments(segments, q)
         slide_size = _norm_window(causal, slide_size, q.shape[2])
         sc = _default_scale(q.shape[3], scale)
-        o, lse = _forward(q, k, v, causal, slide_size, sc, store_lse=True, segments=segments)
+        cap = _check_softcap(softcap)
+        o, lse = _forward(q, k, v, causal, slide_size, sc, store_lse=True, segments=segments, softcap=cap)
         if segments is None:
             ctx.save_for_backward(q, k, v, o, lse)
         else:
@@ -225,6 +238,7 @@ class FlashAttnGQAFunction(torch.autograd.Function):
         ctx.causal = bool(causal)
         ctx.slide_size = slide_size
         ctx.scale = sc
+        ctx.softcap = cap
         return o
 
     @staticmethod
@@ -232,22 +246,24 @@ class FlashAttnGQAFunction(torch.autograd.Function):
         q, k, v, o, lse, *seg = ctx.saved_tensors
         q, k, v = _prep(q), _prep(k), _prep(v)
         dq, dk, dv, _ = _backward(q, k, v, o, lse, do, ctx.causal, ctx.slide_size, ctx.scale,
-                                  segments=tuple(seg) if seg else None)
-        return dq, dk, dv, None, None, None, None
+                                  segments=tuple(seg) if seg else None, softcap=ctx.softcap)
+        return dq, dk, dv, None, None, None, None, None
 
 
-def flash_attn_gqa_train(q, k, v, causal=False, slide_size=0, *, scale=None, segments=None):
+def flash_attn_gqa_train(q, k, v, causal=False, slide_size=0, *, scale=None, segments=None, softcap=None):
     """Flash attention with autograd support (reference attention.py:1625-1635).
 
     q: (B, N_Q_HEADS, N, D); k, v: (B, N_KV_HEADS, N, D); fp16 or bf16; D in {64, 128, 256, 512}.
     ``scale`` defaults to 1/sqrt(D) like the reference; other values are used natively.
     ``segments``: optional (lo, hi) int32 (B, N) tables for ragged batches (segments.py).
+    ``softcap``: optional logit soft-cap (scaled scores x -> softcap * tanh(x / softcap), as
+    transformers' ``softcap``); not in the reference, whose adapter rejects it.
     """
-    return FlashAttnGQAFunction.apply(q, k, v, causal, slide_size, scale, segments)
+    return FlashAttnGQAFunction.apply(q, k, v, causal, slide_size, scale, segments, softcap)
 
 
 def attention_flash_gqa(q, k, v, causal=False, slide_size=0, BLOCK_Q=None, BLOCK_KV=None, BLOCK_D=None,
-                        num_warps=None, num_stages=None, *, scale=None, segments=None):
+                        num_warps=None, num_stages=None, *, scale=None, segments=None, softcap=None):
     """Inference forward without LSE (reference attention.py:540-604). Default causal=False.
 
     ``BLOCK_KV`` selects one of the built LDS tile widths for this head dim. ``BLOCK_Q``,
@@ -267,6 +283,6 @@ def attention_flash_gqa(q, k, v, causal=False, slide_size=0, BLOCK_Q=None, BLOCK
         raise ValueError("BLOCK_D must equal HEAD_DIM (no head-dim tiling)")
     slide_size = _norm_window(causal, slide_size, q.shape[2])
     o, _ = _forward(q, k, v, causal, slide_size, _default_scale(D, scale), store_lse=False, block_kv=bkv,
-                    segments=_check_segments(segments, q))
+                    segments=_check_segments(segments, q), softcap=_check_softcap(softcap))
     return o
 

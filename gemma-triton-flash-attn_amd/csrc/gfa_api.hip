@@ -75,8 +75,24 @@ const Entry* lookup(int d) {
   return nullptr;
 }
 
-bool fwd_built(int d, int bkv, int nw) {
+bool fwd_built(int d, int bkv, int nw, bool cap) {
+  if (cap)  // soft-capped instances: the registry's default tiles
+    return nw == 4 && ((d == 512 && bkv == 32) || (d == 256 && bkv == 32) || (d == 128 && (bkv == 32 || bkv == 64)) ||
+                       (d == 64 && bkv == 64));
   return nw == 4 && ((d == 512 && bkv == 32) || (d <= 256 && (bkv == 32 || bkv == 64)));
+}
+
+// Soft-capping: finite and >= 0 (0 = off); the kernels' multipliers.
+int check_softcap(float softcap) {
+  if (!std::isfinite(softcap) || softcap < 0.f)
+    return fail(GFA_ERR_INVALID_ARGUMENT, "softcap=%g must be finite and >= 0 (0 = off)", (double)softcap);
+  return GFA_OK;
+}
+gfa::SoftCap soft_cap(float scale, float softcap) {
+  gfa::SoftCap c;
+  c.cap_a = softcap > 0.f ? scale / softcap : 0.f;
+  c.cap_log2 = softcap * 1.4426950408889634f;
+  return c;
 }
 
 int largest_pow2_divisor_le(int r, int cap) {
@@ -221,12 +237,15 @@ int gfa_fwd(const gfa_fwd_args* a) {
   if (!std::isfinite(a->scale) || !(a->scale > 0.f))
     return fail(GFA_ERR_INVALID_ARGUMENT, "scale=%g must be finite and positive", (double)a->scale);
   if ((rc = check_segments(a->seg_lo, a->seg_hi))) return rc;
+  if ((rc = check_softcap(a->softcap))) return rc;
+  const bool cap = a->softcap > 0.f;
   const Entry* e = lookup(a->head_dim);
   const bool windowed = is_windowed(a->causal, a->window, a->seq_len);
   const int bkv = a->block_kv ? a->block_kv : (windowed ? e->fwd_bkv_window : e->fwd_bkv);
   const int nw = e->fwd_waves;
-  if (!fwd_built(a->head_dim, bkv, nw))
-    return fail(GFA_ERR_UNSUPPORTED, "no forward kernel built for head_dim=%d block_kv=%d", a->head_dim, bkv);
+  if (!fwd_built(a->head_dim, bkv, nw, cap))
+    return fail(GFA_ERR_UNSUPPORTED, "no forward kernel built for head_dim=%d block_kv=%d%s", a->head_dim, bkv,
+                cap ? " with softcap" : "");
 
   gfa::FwdParams p;
   p.seg_lo = a->seg_lo;
@@ -249,6 +268,7 @@ int gfa_fwd(const gfa_fwd_args* a) {
   // attention.py:1441-1443: a window covering the whole sequence is plain causal.
   p.window = is_windowed(a->causal, a->window, a->seq_len) ? a->window : 0;
   p.scale_log2 = a->scale * 1.4426950408889634f;
+  p.cap = soft_cap(a->scale, a->softcap);
   p.store_lse = a->lse != nullptr;
   p.lse_ld = a->lse_ld;
   if (p.store_lse && (a->lse_ld < GFA_LSE_LD(a->seq_len) || !aligned16(a->lse) || (a->lse_ld & 3)))
@@ -256,7 +276,7 @@ int gfa_fwd(const gfa_fwd_args* a) {
                 GFA_LSE_LD(a->seq_len));
   p.g = make_qgrid(p.B, p.Hkv, p.R, p.N, nw);
   if (p.g.nblocks <= 0) return fail(GFA_ERR_INVALID_ARGUMENT, "empty grid");
-  const hipError_t err = gfa::launch_fwd(p, a->head_dim, bkv, nw, a->dtype == GFA_DTYPE_BF16,
+  const hipError_t err = gfa::launch_fwd(p, a->head_dim, bkv, nw, a->dtype == GFA_DTYPE_BF16, cap,
                                          static_cast<hipStream_t>(a->stream));
   if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "forward launch failed: %s", hipGetErrorString(err));
   return ok();
@@ -304,6 +324,8 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   if (!std::isfinite(a->scale) || !(a->scale > 0.f))
     return fail(GFA_ERR_INVALID_ARGUMENT, "scale=%g must be finite and positive", (double)a->scale);
   if ((rc = check_segments(a->seg_lo, a->seg_hi))) return rc;
+  if ((rc = check_softcap(a->softcap))) return rc;
+  const bool cap = a->softcap > 0.f;
   const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
   if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);
   const Entry* e = lookup(a->head_dim);
@@ -347,11 +369,12 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   pq.window = window;
   pq.scale = a->scale;
   pq.scale_log2 = scale_log2;
+  pq.cap = soft_cap(a->scale, a->softcap);
   pq.lse_ld = a->lse_ld;
   pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves / e->dq_split);
   hipError_t err = hipSuccess;
   if (stages & GFA_BWD_DQ) {
-    err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, e->dq_split, bf16, stream);
+    err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, e->dq_split, bf16, cap, stream);
     if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dQ launch failed: %s", hipGetErrorString(err));
   }
   if (!(stages & GFA_BWD_DKV)) return ok();
@@ -384,13 +407,17 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   pk.scale = a->scale;
   pk.scale_log2 = scale_log2;
   pk.inv_scale = 1.0f / a->scale;
+  pk.cap = pq.cap;
   pk.q_splits = qs;
   pk.lse_ld = a->lse_ld;
-  const DkvForm& f = dkv_form(e, a->causal, a->window, a->seq_len);
+  // Soft-capped problems run the plain-chain form: the windowed D=256 pair starts its chains
+  // from the row statistics and keeps no raw score. The split count stays the shared rule's
+  // (any split is exact), so the workspace size does not depend on the cap.
+  const DkvForm& f = cap ? e->dkv : dkv_form(e, a->causal, a->window, a->seq_len);
   const int keys_per_wg = 32 * (f.waves / f.roles);
   pk.n_kb = (pk.N + keys_per_wg - 1) / keys_per_wg;
   pk.nblocks = (pk.n_kb + 3) / 4 * 4 * pk.B * pk.Hkv * qs;  // key blocks in groups of four (bwd_dkv_kernel)
-  err = gfa::launch_bwd_dkv(pk, a->head_dim, f.bq, f.waves, f.roles, bf16, stream);
+  err = gfa::launch_bwd_dkv(pk, a->head_dim, f.bq, f.waves, f.roles, bf16, cap, stream);
   if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV launch failed: %s", hipGetErrorString(err));
   if (qs > 1) {
     err = gfa::launch_dkv_reduce(pk, a->head_dim, bf16, stream);

@@ -40,7 +40,7 @@ namespace gfa {
 // whole-row copies; per-lane loads in the MFMA operand layout touch 32 rows per instruction.
 constexpr bool dkv_stages_rows(int D, int roles) { return roles == 1 && D >= 128; }
 
-template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE>
+template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE, bool CAP>
 __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParams p) {
   constexpr int KT = D / 16;   // MFMA k-steps of the score products (full head dim)
   constexpr int DB = D / 32;   // 32-row blocks of the dV^T / dK^T accumulator
@@ -207,6 +207,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // the row statistic instead of zero, so neither LSE nor delta stays live past the chain:
   // role 0 from -LSE / scale (P = exp2(scale * log2e * acc)), role 1 from -delta (dS = P acc).
   constexpr bool INIT = ROLES == 2 && D == 256;
+  // CAP (soft-capped scores) needs the raw score, which a chain started from -LSE / scale no
+  // longer holds; the host runs soft-capped problems on the other forms.
+  static_assert(!(CAP && INIT), "soft-capping needs the plain score chain");
   const int roff0 = l32 * (2 * D) + ((h ^ swz<D>(l32)) << 4);  // tile row l32, chunk h (k-step 0)
   int toff0;  // tiles read transposed (A operands of dV^T, dK^T): rows 4h + t/4, column block 0
   int toffA[4], toffB[4];
@@ -325,6 +328,29 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       }
     }
   };
+  // CAP, hand-off form (role 0): P of the capped scores into sc, and P (1 - tanh^2), the factor
+  // role 1 multiplies dP - delta by, into the exchange planes; both masked.
+  auto make_p_cap = [&](f32x16 (&sc)[SB], const f32x4 (&lse)[SB][4], int q0, char GFA_LDS* pxr)
+                        __attribute__((always_inline)) {
+    const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
+#pragma unroll
+    for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * j + e;
+          const float t = cap_tanh(sc[sb][r] * p.cap.cap_a);
+          float pv = fast_exp2(t * p.cap.cap_log2 - lse[sb][j][e] * kLog2e);
+          if (need_mask) pv = vis.has(q0 + sb * 32 + 8 * j + 4 * h + e) ? pv : 0.f;
+          sc[sb][r] = pv;
+          w[e] = pv * (1.f - t * t);
+        }
+        *reinterpret_cast<f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024) = w;
+      }
+    }
+  };
   // dS = P * (dP - delta) in place of dP. Masked entries have P = 0 and give 0: delta is
   // finite on every row a tile covers (the dQ kernel writes the rows past N of the last
   // 32-row block too), so no guard is needed.
@@ -419,10 +445,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
             f32x4 w[2];
   #pragma unroll
             for (int j = 0; j < 2; ++j) w[j] = *reinterpret_cast<const f32x4 GFA_LDS*>(slot(sb, 1 - RO, j));
-            float pv[8], dsv[8];
+            float pv[8], dsv[8], gcap[8];
   #pragma unroll
             for (int i = 0; i < 8; ++i) {
               const float sv = RO == 0 ? s[sb][MH + i] : w[i >> 2][i & 3];
+              if constexpr (CAP) {
+                const float t = cap_tanh(sv * p.cap.cap_a);
+                pv[i] = fast_exp2(t * p.cap.cap_log2 - st[0][sb][i >> 2][i & 3] * kLog2e);
+                gcap[i] = 1.f - t * t;
+                continue;
+              }
               pv[i] = fast_exp2(sv * p.scale_log2 - st[0][sb][i >> 2][i & 3] * kLog2e);
             }
             if (need_mask) {
@@ -436,6 +468,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
             for (int i = 0; i < 8; ++i) {
               const float dpv = RO == 1 ? s[sb][MH + i] : w[i >> 2][i & 3];
               dsv[i] = pv[i] * (dpv - st[0][sb][2 + (i >> 2)][i & 3]);
+              if constexpr (CAP) dsv[i] *= gcap[i];
             }
             // Packed to 16 bits (the accumulations' B operand): the half this role accumulates
             // stays, the half the partner accumulates goes to its slot (role 0: dS, role 1: P).
@@ -461,17 +494,21 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       } else {
         // Hand-off form: role 0 computes P of all rows and hands it to role 1 (fp32).
         if (role == 0) {
-          if constexpr (INIT) {
-            make_p_init(s, q0);
+          if constexpr (CAP) {
+            make_p_cap(s, st[0], q0, pxr);
           } else {
-            make_p(s, st[0], q0);
-          }
+            if constexpr (INIT) {
+              make_p_init(s, q0);
+            } else {
+              make_p(s, st[0], q0);
+            }
   #pragma unroll
-          for (int sb = 0; sb < SB; ++sb) {
+            for (int sb = 0; sb < SB; ++sb) {
   #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const f32x4 v = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
-              *reinterpret_cast<f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024) = v;
+              for (int j = 0; j < 4; ++j) {
+                const f32x4 v = {s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
+                *reinterpret_cast<f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024) = v;
+              }
             }
           }
         }
@@ -528,13 +565,29 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       }
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
-      make_p(s, st[0], q0);
+      if constexpr (CAP) {
+        // P of the capped scores, and dS = P (1 - tanh^2) (dP - delta), element by element.
+        const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
 #pragma unroll
-      for (int sb = 0; sb < SB; ++sb) {
-        f32x4 pv4[4];
+        for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pv4[j] = f32x4{s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
-        make_ds(dp[sb], pv4, st[NS - 1][sb]);
+          for (int r = 0; r < 16; ++r) {
+            const float t = cap_tanh(s[sb][r] * p.cap.cap_a);
+            float pv = fast_exp2(t * p.cap.cap_log2 - st[0][sb][r >> 2][r & 3] * kLog2e);
+            if (need_mask) pv = vis.has(q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) ? pv : 0.f;
+            s[sb][r] = pv;
+            dp[sb][r] = pv * (1.f - t * t) * (dp[sb][r] - st[NS - 1][sb][r >> 2][r & 3]);
+          }
+        }
+      } else {
+        make_p(s, st[0], q0);
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb) {
+          f32x4 pv4[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pv4[j] = f32x4{s[sb][4 * j], s[sb][4 * j + 1], s[sb][4 * j + 2], s[sb][4 * j + 3]};
+          make_ds(dp[sb], pv4, st[NS - 1][sb]);
+        }
       }
       i16x8 pb[BQ / 16], dsb[BQ / 16];
       pack(s, pb);
@@ -741,39 +794,50 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const BwdDkvParams p, i
 }
 
 // Explicit instantiations of every built variant (device code and host launch stubs).
-#define GFA_DKV_INST(DD, BB, WW, RR, EE)                                              \
-  template __global__ void bwd_dkv_kernel<DD, BB, true, WW, RR, EE>(const BwdDkvParams);  \
-  template __global__ void bwd_dkv_kernel<DD, BB, false, WW, RR, EE>(const BwdDkvParams);
-GFA_DKV_INST(512, 32, 4, 2, 1)
-GFA_DKV_INST(256, 32, 4, 1, 1)
-GFA_DKV_INST(256, 32, 4, 2, 2)
-GFA_DKV_INST(64, 32, 4, 1, 2)
-GFA_DKV_INST(128, 32, 4, 2, 2)
+#define GFA_DKV_INST(DD, BB, WW, RR, EE, CC)                                              \
+  template __global__ void bwd_dkv_kernel<DD, BB, true, WW, RR, EE, CC>(const BwdDkvParams);  \
+  template __global__ void bwd_dkv_kernel<DD, BB, false, WW, RR, EE, CC>(const BwdDkvParams);
+GFA_DKV_INST(512, 32, 4, 2, 1, false)
+GFA_DKV_INST(256, 32, 4, 1, 1, false)
+GFA_DKV_INST(256, 32, 4, 2, 2, false)
+GFA_DKV_INST(64, 32, 4, 1, 2, false)
+GFA_DKV_INST(128, 32, 4, 2, 2, false)
+// Soft-capped instances (D=256 runs the one-wave form; the windowed pair starts its chains from
+// the row statistics).
+GFA_DKV_INST(512, 32, 4, 2, 1, true)
+GFA_DKV_INST(256, 32, 4, 1, 1, true)
+GFA_DKV_INST(64, 32, 4, 1, 2, true)
+GFA_DKV_INST(128, 32, 4, 2, 2, true)
 #undef GFA_DKV_INST
 template __global__ void dkv_reduce_kernel<true>(const BwdDkvParams, int);
 template __global__ void dkv_reduce_kernel<false>(const BwdDkvParams, int);
 
-template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE>
+template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE, bool CAP>
 static hipError_t launch_dkv_t(const BwdDkvParams& p, hipStream_t stream) {
   const unsigned stage_bytes = dkv_stages_rows(D, ROLES) ? NW * BQ * D * 2 : 0;  // the kernel's stage_raw
-  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW, ROLES, WPE>), dim3(p.nblocks), dim3(NW * 64), stage_bytes, stream,
-                     p);
+  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW, ROLES, WPE, CAP>), dim3(p.nblocks), dim3(NW * 64), stage_bytes,
+                     stream, p);
   return hipGetLastError();
 }
 
 // Built dK/dV variants: (head dim, queries per tile, waves per workgroup, waves per 32 keys,
 // waves per SIMD).
-hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, int nw, int roles, bool bf16, hipStream_t stream) {
-#define GFA_DKV_CASE(DD, BB, WW, RR, EE)                                                   \
-  if (D == DD && bq == BB && nw == WW && roles == RR) {                                    \
-    return bf16 ? launch_dkv_t<DD, BB, true, WW, RR, EE>(p, stream)                        \
-                : launch_dkv_t<DD, BB, false, WW, RR, EE>(p, stream);                      \
+hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, int nw, int roles, bool bf16, bool cap,
+                          hipStream_t stream) {
+#define GFA_DKV_CASE(DD, BB, WW, RR, EE, CC)                                               \
+  if (D == DD && bq == BB && nw == WW && roles == RR && cap == CC) {                       \
+    return bf16 ? launch_dkv_t<DD, BB, true, WW, RR, EE, CC>(p, stream)                    \
+                : launch_dkv_t<DD, BB, false, WW, RR, EE, CC>(p, stream);                  \
   }
-  GFA_DKV_CASE(512, 32, 4, 2, 1)
-  GFA_DKV_CASE(256, 32, 4, 1, 1)
-  GFA_DKV_CASE(256, 32, 4, 2, 2)
-  GFA_DKV_CASE(64, 32, 4, 1, 2)
-  GFA_DKV_CASE(128, 32, 4, 2, 2)
+  GFA_DKV_CASE(512, 32, 4, 2, 1, false)
+  GFA_DKV_CASE(256, 32, 4, 1, 1, false)
+  GFA_DKV_CASE(256, 32, 4, 2, 2, false)
+  GFA_DKV_CASE(64, 32, 4, 1, 2, false)
+  GFA_DKV_CASE(128, 32, 4, 2, 2, false)
+  GFA_DKV_CASE(512, 32, 4, 2, 1, true)
+  GFA_DKV_CASE(256, 32, 4, 1, 1, true)
+  GFA_DKV_CASE(64, 32, 4, 1, 2, true)
+  GFA_DKV_CASE(128, 32, 4, 2, 2, true)
 #undef GFA_DKV_CASE
   return hipErrorInvalidValue;
 }

@@ -27,7 +27,7 @@ namespace gfa {
 // there only adds a barrier and a round trip (measured 0.7% slower).
 constexpr bool dq_stages_rows(int D, int split) { return split == 1 && D >= 128; }
 
-template <int D, int BKV, bool IS_BF16, int NW, int SPLIT>
+template <int D, int BKV, bool IS_BF16, int NW, int SPLIT, bool CAP>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p) {
   constexpr int DH = D / SPLIT;  // head-dim slice of dQ^T one wave accumulates
   constexpr int KT = D / 16;     // k-steps of a score chain (always the full head dim)
@@ -236,6 +236,16 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 #pragma unroll
   for (int i = 0; i < DBH; ++i) acc[i] = f32x16{};
 
+  // P of a raw score, times dS's soft-cap factor 1 - tanh^2 with CAP (so dS = this * (dP - delta)).
+  auto p_of = [&](float sv) __attribute__((always_inline)) {
+    if constexpr (CAP) {
+      const float t = cap_tanh(sv * p.cap.cap_a);
+      return fast_exp2(t * p.cap.cap_log2 - lse_log2) * (1.f - t * t);
+    } else {
+      return fast_exp2(sv * p.scale_log2 - lse_log2);
+    }
+  };
+
   int toffA[4], toffB[4];  // K tile read transposed (A operand of dQ^T = K^T dS^T)
   {
     const int t16 = lane & 15;
@@ -285,7 +295,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       for (int i = 0; i < 8; ++i) {
         const float sv = RO == 0 ? own[sb][MH + i] : w[i >> 2][i & 3];
         const float dpv = RO == 1 ? own[sb][MH + i] : w[i >> 2][i & 3];
-        ds[i] = fast_exp2(sv * p.scale_log2 - lse_log2) * (DP_FROM_DELTA ? dpv : dpv - delta_left);
+        ds[i] = p_of(sv) * (DP_FROM_DELTA ? dpv : dpv - delta_left);
       }
       if (need_mask) {
 #pragma unroll
@@ -371,7 +381,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float dpd = DP_FROM_DELTA ? dp[sb][r] : dp[sb][r] - delta_left;
-        s[sb][r] = fast_exp2(s[sb][r] * p.scale_log2 - lse_log2) * dpd;
+        s[sb][r] = p_of(s[sb][r]) * dpd;
       }
     }
     if (need_mask) {
@@ -457,33 +467,42 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   }
 }
 
-// Explicit instantiations of every built variant (device code and host launch stubs).
-template __global__ void bwd_dq_kernel<512, 32, true, 4, 2>(const BwdDqParams);
-template __global__ void bwd_dq_kernel<512, 32, false, 4, 2>(const BwdDqParams);
-template __global__ void bwd_dq_kernel<256, 32, true, 4, 1>(const BwdDqParams);
-template __global__ void bwd_dq_kernel<256, 32, false, 4, 1>(const BwdDqParams);
-template __global__ void bwd_dq_kernel<128, 32, true, 4, 1>(const BwdDqParams);
-template __global__ void bwd_dq_kernel<128, 32, false, 4, 1>(const BwdDqParams);
-template __global__ void bwd_dq_kernel<64, 32, true, 4, 1>(const BwdDqParams);
-template __global__ void bwd_dq_kernel<64, 32, false, 4, 1>(const BwdDqParams);
+// Explicit instantiations of every built variant (device code and host launch stubs), plain and
+// soft-capped.
+#define GFA_DQ_INST(DD, SS)                                                          \
+  template __global__ void bwd_dq_kernel<DD, 32, true, 4, SS, false>(const BwdDqParams);  \
+  template __global__ void bwd_dq_kernel<DD, 32, false, 4, SS, false>(const BwdDqParams); \
+  template __global__ void bwd_dq_kernel<DD, 32, true, 4, SS, true>(const BwdDqParams);   \
+  template __global__ void bwd_dq_kernel<DD, 32, false, 4, SS, true>(const BwdDqParams);
+GFA_DQ_INST(512, 2)
+GFA_DQ_INST(256, 1)
+GFA_DQ_INST(128, 1)
+GFA_DQ_INST(64, 1)
+#undef GFA_DQ_INST
 
 template <int D, int BKV, bool IS_BF16, int NW, int SPLIT>
-static hipError_t launch_dq_t(const BwdDqParams& p, hipStream_t stream) {
+static hipError_t launch_dq_t(const BwdDqParams& p, bool cap, hipStream_t stream) {
   const unsigned stage_bytes = dq_stages_rows(D, SPLIT) ? NW * BKV * D * 2 : 0;  // the kernel's stage_raw
-  hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT>), dim3(p.g.nblocks), dim3(NW * 64), stage_bytes, stream, p);
+  if (cap) {
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, true>), dim3(p.g.nblocks), dim3(NW * 64), stage_bytes,
+                       stream, p);
+  } else {
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, false>), dim3(p.g.nblocks), dim3(NW * 64), stage_bytes,
+                       stream, p);
+  }
   return hipGetLastError();
 }
 
 // Built dQ variants: D=512 on wave pairs (head-dim halves), D=256/128/64 one wave per 32 rows.
-hipError_t launch_bwd_dq(const BwdDqParams& p, int D, int bkv, int split, bool bf16, hipStream_t stream) {
+hipError_t launch_bwd_dq(const BwdDqParams& p, int D, int bkv, int split, bool bf16, bool cap, hipStream_t stream) {
   if (D == 512 && bkv == 32 && split == 2)
-    return bf16 ? launch_dq_t<512, 32, true, 4, 2>(p, stream) : launch_dq_t<512, 32, false, 4, 2>(p, stream);
+    return bf16 ? launch_dq_t<512, 32, true, 4, 2>(p, cap, stream) : launch_dq_t<512, 32, false, 4, 2>(p, cap, stream);
   if (D == 256 && bkv == 32 && split == 1)
-    return bf16 ? launch_dq_t<256, 32, true, 4, 1>(p, stream) : launch_dq_t<256, 32, false, 4, 1>(p, stream);
+    return bf16 ? launch_dq_t<256, 32, true, 4, 1>(p, cap, stream) : launch_dq_t<256, 32, false, 4, 1>(p, cap, stream);
   if (D == 128 && bkv == 32 && split == 1)
-    return bf16 ? launch_dq_t<128, 32, true, 4, 1>(p, stream) : launch_dq_t<128, 32, false, 4, 1>(p, stream);
+    return bf16 ? launch_dq_t<128, 32, true, 4, 1>(p, cap, stream) : launch_dq_t<128, 32, false, 4, 1>(p, cap, stream);
   if (D == 64 && bkv == 32 && split == 1)
-    return bf16 ? launch_dq_t<64, 32, true, 4, 1>(p, stream) : launch_dq_t<64, 32, false, 4, 1>(p, stream);
+    return bf16 ? launch_dq_t<64, 32, true, 4, 1>(p, cap, stream) : launch_dq_t<64, 32, false, 4, 1>(p, cap, stream);
   return hipErrorInvalidValue;
 }
 

@@ -61,6 +61,13 @@ __device__ __forceinline__ float from16(short x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// tanh(x) = 1 - 2 / (exp(2x) + 1): one exp2 and one reciprocal (v_exp_f32, v_rcp_f32),
+// exactly +-1 once exp(2x) overflows or underflows; absolute error about 1e-7.
+__device__ __forceinline__ float cap_tanh(float x) {
+  const float e = fast_exp2(x * 2.8853900817779268f);  // exp(2x) = exp2(2x log2(e))
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+}
+
 // Combine a value with the one held by the lane 32 apart (the other half of a 32-row
 // fragment): v_permlane32_swap exchanges the wave halves in registers, without an LDS
 // round trip. Both lanes of a pair get the same result.

@@ -38,7 +38,7 @@
 
 namespace gfa {
 
-template <int D, int BKV, bool IS_BF16, int NW, int WPE, bool SEG>
+template <int D, int BKV, bool IS_BF16, int NW, int WPE, bool SEG, bool CAP>
 __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   constexpr int KT = D / 16;   // MFMA k-steps over the head dim
   constexpr int DB = D / 32;   // 32-row blocks of the O^T accumulator
@@ -207,6 +207,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     for (int sb = 1; sb < SB; ++sb) s[sb] = mma_chain1_lds_b<IS_BF16, KT, 4>(kt, koff0, sb * 32 * (2 * D), qf);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(0);
+    // CAP: soft-capped scores. The tile now holds tanh(scale s / softcap); the exponent
+    // multiplier below is softcap log2(e) instead of scale log2(e).
+    if constexpr (CAP) {
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[sb][r] = cap_tanh(s[sb][r] * p.cap.cap_a);
+      }
+    }
+    const float xs = CAP ? p.cap.cap_log2 : p.scale_log2;
 
     const bool need_mask = !(active && k0 + BKV <= all_hi && k0 >= all_lo);
     if (need_mask) {
@@ -233,7 +243,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) m = fmaxf(m, s[sb][r]);
       }
-      return halves_max(m) * p.scale_log2;
+      return halves_max(m) * xs;
     };
     if constexpr (MODE == 1) {
       m_seen = fmaxf(m_seen, row_max());
@@ -253,7 +263,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = fast_exp2(s[sb][r] * p.scale_log2 - m_ref);
+        const float pv = fast_exp2(s[sb][r] * xs - m_ref);
         l_run += pv;
         pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
       }
@@ -343,45 +353,57 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
 
 // Explicit instantiations of every built variant (both the device code and the host
 // launch stubs must exist for each one).
-#define GFA_FWD_INST(DD, BB, WW, EE)                                                  \
-  template __global__ void fwd_kernel<DD, BB, true, WW, EE, false>(const FwdParams);  \
-  template __global__ void fwd_kernel<DD, BB, false, WW, EE, false>(const FwdParams); \
-  template __global__ void fwd_kernel<DD, BB, true, WW, EE, true>(const FwdParams);   \
-  template __global__ void fwd_kernel<DD, BB, false, WW, EE, true>(const FwdParams);
-GFA_FWD_INST(512, 32, 4, 1)
-GFA_FWD_INST(256, 64, 4, 1)
-GFA_FWD_INST(256, 32, 4, 1)
-GFA_FWD_INST(256, 32, 4, 2)
-GFA_FWD_INST(128, 64, 4, 2)
-GFA_FWD_INST(128, 32, 4, 2)
-GFA_FWD_INST(64, 64, 4, 3)
-GFA_FWD_INST(64, 32, 4, 3)
+#define GFA_FWD_INST(DD, BB, WW, EE, CC)                                                  \
+  template __global__ void fwd_kernel<DD, BB, true, WW, EE, false, CC>(const FwdParams);  \
+  template __global__ void fwd_kernel<DD, BB, false, WW, EE, false, CC>(const FwdParams); \
+  template __global__ void fwd_kernel<DD, BB, true, WW, EE, true, CC>(const FwdParams);   \
+  template __global__ void fwd_kernel<DD, BB, false, WW, EE, true, CC>(const FwdParams);
+GFA_FWD_INST(512, 32, 4, 1, false)
+GFA_FWD_INST(256, 64, 4, 1, false)
+GFA_FWD_INST(256, 32, 4, 1, false)
+GFA_FWD_INST(256, 32, 4, 2, false)
+GFA_FWD_INST(128, 64, 4, 2, false)
+GFA_FWD_INST(128, 32, 4, 2, false)
+GFA_FWD_INST(64, 64, 4, 3, false)
+GFA_FWD_INST(64, 32, 4, 3, false)
+// Soft-capped instances: the registry's default tiles only.
+GFA_FWD_INST(512, 32, 4, 1, true)
+GFA_FWD_INST(256, 32, 4, 2, true)
+GFA_FWD_INST(128, 64, 4, 2, true)
+GFA_FWD_INST(128, 32, 4, 2, true)
+GFA_FWD_INST(64, 64, 4, 3, true)
 #undef GFA_FWD_INST
 
-template <int D, int BKV, bool IS_BF16, int NW, int WPE>
+template <int D, int BKV, bool IS_BF16, int NW, int WPE, bool CAP>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   if (p.seg_lo != nullptr) {
-    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, true>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
+    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, true, CAP>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
   } else {
-    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, false>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
+    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, false, CAP>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream,
+                       p);
   }
   return hipGetLastError();
 }
 
 // Built forward variants: (head dim, keys per tile, waves per workgroup, waves per SIMD).
-hipError_t launch_fwd(const FwdParams& p, int D, int bkv, int nw, bool bf16, hipStream_t stream) {
-#define GFA_FWD_CASE(DD, BB, WW, EE)                                                      \
-  if (D == DD && bkv == BB && nw == WW) {                                                 \
-    return bf16 ? launch_fwd_t<DD, BB, true, WW, EE>(p, stream)                           \
-                : launch_fwd_t<DD, BB, false, WW, EE>(p, stream);                         \
+hipError_t launch_fwd(const FwdParams& p, int D, int bkv, int nw, bool bf16, bool cap, hipStream_t stream) {
+#define GFA_FWD_CASE(DD, BB, WW, EE, CC)                                                  \
+  if (D == DD && bkv == BB && nw == WW && cap == CC) {                                    \
+    return bf16 ? launch_fwd_t<DD, BB, true, WW, EE, CC>(p, stream)                       \
+                : launch_fwd_t<DD, BB, false, WW, EE, CC>(p, stream);                     \
   }
-  GFA_FWD_CASE(512, 32, 4, 1)
-  GFA_FWD_CASE(256, 64, 4, 1)
-  GFA_FWD_CASE(256, 32, 4, 2)
-  GFA_FWD_CASE(128, 64, 4, 2)
-  GFA_FWD_CASE(128, 32, 4, 2)
-  GFA_FWD_CASE(64, 64, 4, 3)
-  GFA_FWD_CASE(64, 32, 4, 3)
+  GFA_FWD_CASE(512, 32, 4, 1, false)
+  GFA_FWD_CASE(256, 64, 4, 1, false)
+  GFA_FWD_CASE(256, 32, 4, 2, false)
+  GFA_FWD_CASE(128, 64, 4, 2, false)
+  GFA_FWD_CASE(128, 32, 4, 2, false)
+  GFA_FWD_CASE(64, 64, 4, 3, false)
+  GFA_FWD_CASE(64, 32, 4, 3, false)
+  GFA_FWD_CASE(512, 32, 4, 1, true)
+  GFA_FWD_CASE(256, 32, 4, 2, true)
+  GFA_FWD_CASE(128, 64, 4, 2, true)
+  GFA_FWD_CASE(128, 32, 4, 2, true)
+  GFA_FWD_CASE(64, 64, 4, 3, true)
 #undef GFA_FWD_CASE
   return hipErrorInvalidValue;
 }

@@ -11,6 +11,15 @@ struct RowView {
   int64_t sb, sh, sn;
 };
 
+// Logit soft-capping (the kernels' CAP instances): a raw score s = q.k becomes
+// (softcap / scale) * tanh(s * cap_a), i.e. the scaled score scale * s becomes
+// softcap * tanh(scale * s / softcap); the softmax exponent of the capped score is
+// tanh(...) * cap_log2 in the log2 domain, and dS carries the factor 1 - tanh^2.
+struct SoftCap {
+  float cap_a;     // scale / softcap
+  float cap_log2;  // softcap * log2(e)
+};
+
 // Work decomposition shared by the forward and dQ kernels: a workgroup owns
 // NWAVES (head, 32-query block) pairs of one KV head: `hpw` heads x `qbw` query blocks.
 struct QGrid {
@@ -37,6 +46,7 @@ struct FwdParams {
   int causal;
   int window;        // 0 = no sliding window; only honoured when causal
   float scale_log2;  // softmax scale * log2(e)
+  SoftCap cap;       // read by the CAP instances only
   int store_lse;
   int lse_ld;
   QGrid g;
@@ -58,6 +68,7 @@ struct BwdDqParams {
   int causal, window;
   float scale;       // softmax scale (applied to dQ at the end)
   float scale_log2;  // scale * log2(e)
+  SoftCap cap;       // read by the CAP instances only
   int lse_ld;
   QGrid g;
 };
@@ -79,6 +90,7 @@ struct BwdDkvParams {
   int causal, window;
   float scale, scale_log2;
   float inv_scale;   // 1 / scale
+  SoftCap cap;       // read by the CAP instances only
   int q_splits;
   int lse_ld;
   int n_kb;          // number of key blocks (each WKV keys wide)

@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define GFA_VERSION 102 /* 1.0.2: optional segment tables (variable-length / padded batches) */
+#define GFA_VERSION 103 /* 1.0.3: optional logit soft-capping (softcap) */
 
 typedef enum {
   GFA_DTYPE_FP16 = 0,
@@ -92,6 +92,9 @@ typedef struct {
   void* stream;        /* hipStream_t */
   const int32_t* seg_lo; /* optional (B, N) segment table (see above); NULL = one segment per row */
   const int32_t* seg_hi;
+  float softcap;       /* 0 = off; > 0: every scaled score x = scale q.k becomes softcap tanh(x / softcap)
+                          before the mask and softmax (transformers' logit soft-capping; the reference
+                          has none). Runs the registry's default tiles (block_kv must be 0 or it). */
 } gfa_fwd_args;
 
 typedef struct {
@@ -121,6 +124,7 @@ typedef struct {
   void* stream;
   const int32_t* seg_lo;  /* the forward's segment table, or NULL */
   const int32_t* seg_hi;
+  float softcap;          /* the forward's soft-cap (0 = off) */
 } gfa_bwd_args;
 
 /* Tile configuration the library uses for one problem (mirrors the Python registry). */

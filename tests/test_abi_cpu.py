@@ -50,8 +50,9 @@ def test_struct_layout_matches_c(tmp_path):
 #include "{HEADER}"
 int main(void) {{
   printf("%zu %zu %zu\\n", sizeof(gfa_fwd_args), sizeof(gfa_bwd_args), sizeof(gfa_config_info));
-  printf("%zu %zu %zu %zu\\n", offsetof(gfa_fwd_args, lse_ld), offsetof(gfa_fwd_args, stream),
-         offsetof(gfa_bwd_args, stages), offsetof(gfa_bwd_args, workspace_bytes));
+  printf("%zu %zu %zu %zu %zu %zu\\n", offsetof(gfa_fwd_args, lse_ld), offsetof(gfa_fwd_args, stream),
+         offsetof(gfa_bwd_args, stages), offsetof(gfa_bwd_args, workspace_bytes),
+         offsetof(gfa_fwd_args, softcap), offsetof(gfa_bwd_args, softcap));
   return 0;
 }}
 ''')
@@ -61,7 +62,7 @@ int main(void) {{
     sizes = [int(x) for x in out]
     assert sizes[:3] == [ctypes.sizeof(_lib.FwdArgs), ctypes.sizeof(_lib.BwdArgs), ctypes.sizeof(_lib.ConfigInfo)]
     assert sizes[3:] == [_lib.FwdArgs.lse_ld.offset, _lib.FwdArgs.stream.offset, _lib.BwdArgs.stages.offset,
-                         _lib.BwdArgs.workspace_bytes.offset]
+                         _lib.BwdArgs.workspace_bytes.offset, _lib.FwdArgs.softcap.offset, _lib.BwdArgs.softcap.offset]
 
 
 @pytest.mark.parametrize("shape", [(1, 32, 4, 16384, 512), (1, 16, 8, 16384, 256), (2, 6, 3, 33, 256),
@@ -114,6 +115,9 @@ def _fwd_args(**over):
     (dict(scale=0.0), 1),                 # the kernels mask with -inf before scaling: scale > 0
     (dict(scale=-0.125), 1),
     (dict(block_kv=48), 2),               # no such forward tile
+    (dict(softcap=float("nan")), 1),
+    (dict(softcap=-1.0), 1),
+    (dict(head_dim=256, block_kv=64, softcap=5.0), 2),  # soft-capping runs the default tiles only
     (dict(k_strides=_lib.Strides(8, 8, 4)), 1),  # row stride not a multiple of 8 elements
 ])
 def test_fwd_rejects_bad_arguments(over, status):
@@ -189,8 +193,6 @@ def test_hf_adapter_rejects_unsupported_features():
 
     mod = SimpleNamespace(head_dim=256, is_causal=True)
     q = torch.zeros(1, 2, 4, 256)
-    with pytest.raises(NotImplementedError):
-        gfa.triton_gqa_attention(mod, q, q, q, None, softcap=30.0)
     with pytest.raises(NotImplementedError):
         gfa.triton_gqa_attention(mod, q, q, q, None, dropout=0.1)
 
