@@ -57,7 +57,7 @@ class FwdArgs(ctypes.Structure):
         ("causal", ctypes.c_int32), ("window", ctypes.c_int32), ("scale", ctypes.c_float),
         ("dtype", ctypes.c_int32), ("block_kv", ctypes.c_int32), ("lse_ld", ctypes.c_int32),
         ("stream", ctypes.c_void_p), ("seg_lo", ctypes.c_void_p), ("seg_hi", ctypes.c_void_p),
-        ("softcap", ctypes.c_float),
+        ("softcap", ctypes.c_float), ("dropout_p", ctypes.c_float), ("dropout_seed", ctypes.c_uint64),
     ]
 
 
@@ -76,7 +76,7 @@ class BwdArgs(ctypes.Structure):
         ("stages", ctypes.c_int32),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("stream", ctypes.c_void_p), ("seg_lo", ctypes.c_void_p), ("seg_hi", ctypes.c_void_p),
-        ("softcap", ctypes.c_float),
+        ("softcap", ctypes.c_float), ("dropout_p", ctypes.c_float), ("dropout_seed", ctypes.c_uint64),
     ]
 
 

@@ -132,8 +132,22 @@ def _check_softcap(softcap) -> float:
     return c
 
 
+def _check_dropout(p) -> float:
+    """Attention dropout probability in [0, 1) (0 = off)."""
+    c = float(p or 0.0)
+    if not math.isfinite(c) or c < 0.0 or c >= 1.0:
+        raise ValueError(f"dropout_p={p} must be in [0, 1)")
+    return c
+
+
+def _dropout_seed() -> int:
+    """A fresh 63-bit mask seed from torch's default (CPU) generator: reproducible under
+    torch.manual_seed, and the same value is handed to the backward."""
+    return int(torch.randint(0, 2 ** 63 - 1, (1,)).item())
+
+
 def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bool, block_kv: int = 0,
-             segments=None, softcap: float = 0.0):
+             segments=None, softcap: float = 0.0, dropout_p: float = 0.0, dropout_seed: int = 0):
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     q, k, v = _prep(q), _prep(k), _prep(v)
@@ -154,6 +168,7 @@ def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bo
     a.block_kv = int(block_kv)
     a.lse_ld = ld
     a.softcap = float(softcap)
+    a.dropout_p, a.dropout_seed = float(dropout_p), int(dropout_seed)
     a.stream = _stream(q.device)
     if segments is not None:
         a.seg_lo, a.seg_hi = segments[0].data_ptr(), segments[1].data_ptr()
@@ -163,7 +178,8 @@ def _forward(q, k, v, causal: bool, slide_size: int, scale: float, store_lse: bo
 
 
 def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, q_splits: int = 0,
-              stages: int = 0, out=None, noalloc: bool = False, segments=None, softcap: float = 0.0):
+              stages: int = 0, out=None, noalloc: bool = False, segments=None, softcap: float = 0.0,
+              dropout_p: float = 0.0, dropout_seed: int = 0):
     """Run gfa_bwd. ``stages`` selects kernels (0 = all; GFA_BWD_DQ / GFA_BWD_DKV bits);
     ``out`` = (dq, dk, dv, delta) reuses caller buffers (profiling a single stage).
     ``noalloc`` calls gfa_bwd_noalloc instead: delta and the workspace then live in the
@@ -203,6 +219,7 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
     a.workspace = ws.data_ptr() if ws is not None else None
     a.workspace_bytes = ws_bytes
     a.softcap = float(softcap)
+    a.dropout_p, a.dropout_seed = float(dropout_p), int(dropout_seed)
     a.stream = _stream(q.device)
     if segments is not None:
         a.seg_lo, a.seg_hi = segments[0].data_ptr(), segments[1].data_ptr()
@@ -224,13 +241,16 @@ class FlashAttnGQAFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, causal=False, slide_size=0, scale=None, segments=None, softcap=None):
+    def forward(ctx, q, k, v, causal=False, slide_size=0, scale=None, segments=None, softcap=None, dropout_p=0.0):
         _check_inputs(q, k, v)
         segments = _check_segments(segments, q)
         slide_size = _norm_window(causal, slide_size, q.shape[2])
         sc = _default_scale(q.shape[3], scale)
         cap = _check_softcap(softcap)
-        o, lse = _forward(q, k, v, causal, slide_size, sc, store_lse=True, segments=segments, softcap=cap)
+        dp = _check_dropout(dropout_p)
+        seed = _dropout_seed() if dp > 0.0 else 0
+        o, lse = _forward(q, k, v, causal, slide_size, sc, store_lse=True, segments=segments, softcap=cap,
+                          dropout_p=dp, dropout_seed=seed)
         if segments is None:
             ctx.save_for_backward(q, k, v, o, lse)
         else:
@@ -239,6 +259,7 @@ class FlashAttnGQAFunction(torch.autograd.Function):
         ctx.slide_size = slide_size
         ctx.scale = sc
         ctx.softcap = cap
+        ctx.dropout = (dp, seed)
         return o
 
     @staticmethod
@@ -246,11 +267,13 @@ class FlashAttnGQAFunction(torch.autograd.Function):
         q, k, v, o, lse, *seg = ctx.saved_tensors
         q, k, v = _prep(q), _prep(k), _prep(v)
         dq, dk, dv, _ = _backward(q, k, v, o, lse, do, ctx.causal, ctx.slide_size, ctx.scale,
-                                  segments=tuple(seg) if seg else None, softcap=ctx.softcap)
-        return dq, dk, dv, None, None, None, None, None
+                                  segments=tuple(seg) if seg else None, softcap=ctx.softcap,
+                                  dropout_p=ctx.dropout[0], dropout_seed=ctx.dropout[1])
+        return dq, dk, dv, None, None, None, None, None, None
 
 
-def flash_attn_gqa_train(q, k, v, causal=False, slide_size=0, *, scale=None, segments=None, softcap=None):
+def flash_attn_gqa_train(q, k, v, causal=False, slide_size=0, *, scale=None, segments=None, softcap=None,
+                         dropout_p=0.0):
     """Flash attention with autograd support (reference attention.py:1625-1635).
 
     q: (B, N_Q_HEADS, N, D); k, v: (B, N_KV_HEADS, N, D); fp16 or bf16; D in {64, 128, 256, 512}.
@@ -258,8 +281,10 @@ def flash_attn_gqa_train(q, k, v, causal=False, slide_size=0, *, scale=None, seg
     ``segments``: optional (lo, hi) int32 (B, N) tables for ragged batches (segments.py).
     ``softcap``: optional logit soft-cap (scaled scores x -> softcap * tanh(x / softcap), as
     transformers' ``softcap``); not in the reference, whose adapter rejects it.
+    ``dropout_p``: attention dropout on the softmax probabilities (kept ones scaled by
+    1 / (1 - p)), with a fresh mask seed from torch's generator per call; not in the reference.
     """
-    return FlashAttnGQAFunction.apply(q, k, v, causal, slide_size, scale, segments, softcap)
+    return FlashAttnGQAFunction.apply(q, k, v, causal, slide_size, scale, segments, softcap, dropout_p)
 
 
 def attention_flash_gqa(q, k, v, causal=False, slide_size=0, BLOCK_Q=None, BLOCK_KV=None, BLOCK_D=None,

@@ -88,6 +88,22 @@ int check_softcap(float softcap) {
     return fail(GFA_ERR_INVALID_ARGUMENT, "softcap=%g must be finite and >= 0 (0 = off)", (double)softcap);
   return GFA_OK;
 }
+// Dropout probability in [0, 1) (0 = off), not together with soft-capping.
+int check_dropout(float p, float softcap) {
+  if (!std::isfinite(p) || p < 0.f || p >= 1.f)
+    return fail(GFA_ERR_INVALID_ARGUMENT, "dropout_p=%g must be in [0, 1)", (double)p);
+  if (p > 0.f && softcap > 0.f) return fail(GFA_ERR_UNSUPPORTED, "dropout together with softcap is not built");
+  return GFA_OK;
+}
+gfa::Dropout dropout_of(float p, uint64_t seed) {
+  gfa::Dropout d;
+  d.seed_lo = (unsigned)(seed & 0xffffffffu);
+  d.seed_hi = (unsigned)(seed >> 32);
+  const double t = (double)p * 4294967296.0;
+  d.thresh = p > 0.f ? (unsigned)std::min(t, 4294967295.0) : 0u;
+  d.inv_keep = 1.0f / (1.0f - p);
+  return d;
+}
 gfa::SoftCap soft_cap(float scale, float softcap) {
   gfa::SoftCap c;
   c.cap_a = softcap > 0.f ? scale / softcap : 0.f;
@@ -238,14 +254,16 @@ int gfa_fwd(const gfa_fwd_args* a) {
     return fail(GFA_ERR_INVALID_ARGUMENT, "scale=%g must be finite and positive", (double)a->scale);
   if ((rc = check_segments(a->seg_lo, a->seg_hi))) return rc;
   if ((rc = check_softcap(a->softcap))) return rc;
+  if ((rc = check_dropout(a->dropout_p, a->softcap))) return rc;
   const bool cap = a->softcap > 0.f;
+  const bool drop = a->dropout_p > 0.f;
   const Entry* e = lookup(a->head_dim);
   const bool windowed = is_windowed(a->causal, a->window, a->seq_len);
   const int bkv = a->block_kv ? a->block_kv : (windowed ? e->fwd_bkv_window : e->fwd_bkv);
   const int nw = e->fwd_waves;
-  if (!fwd_built(a->head_dim, bkv, nw, cap))
+  if (!fwd_built(a->head_dim, bkv, nw, cap || drop))
     return fail(GFA_ERR_UNSUPPORTED, "no forward kernel built for head_dim=%d block_kv=%d%s", a->head_dim, bkv,
-                cap ? " with softcap" : "");
+                cap ? " with softcap" : drop ? " with dropout" : "");
 
   gfa::FwdParams p;
   p.seg_lo = a->seg_lo;
@@ -269,6 +287,7 @@ int gfa_fwd(const gfa_fwd_args* a) {
   p.window = is_windowed(a->causal, a->window, a->seq_len) ? a->window : 0;
   p.scale_log2 = a->scale * 1.4426950408889634f;
   p.cap = soft_cap(a->scale, a->softcap);
+  p.drop = dropout_of(a->dropout_p, a->dropout_seed);
   p.store_lse = a->lse != nullptr;
   p.lse_ld = a->lse_ld;
   if (p.store_lse && (a->lse_ld < GFA_LSE_LD(a->seq_len) || !aligned16(a->lse) || (a->lse_ld & 3)))
@@ -276,7 +295,7 @@ int gfa_fwd(const gfa_fwd_args* a) {
                 GFA_LSE_LD(a->seq_len));
   p.g = make_qgrid(p.B, p.Hkv, p.R, p.N, nw);
   if (p.g.nblocks <= 0) return fail(GFA_ERR_INVALID_ARGUMENT, "empty grid");
-  const hipError_t err = gfa::launch_fwd(p, a->head_dim, bkv, nw, a->dtype == GFA_DTYPE_BF16, cap,
+  const hipError_t err = gfa::launch_fwd(p, a->head_dim, bkv, nw, a->dtype == GFA_DTYPE_BF16, cap, drop,
                                          static_cast<hipStream_t>(a->stream));
   if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "forward launch failed: %s", hipGetErrorString(err));
   return ok();
@@ -325,7 +344,9 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
     return fail(GFA_ERR_INVALID_ARGUMENT, "scale=%g must be finite and positive", (double)a->scale);
   if ((rc = check_segments(a->seg_lo, a->seg_hi))) return rc;
   if ((rc = check_softcap(a->softcap))) return rc;
+  if ((rc = check_dropout(a->dropout_p, a->softcap))) return rc;
   const bool cap = a->softcap > 0.f;
+  const bool drop = a->dropout_p > 0.f;
   const int stages = a->stages ? a->stages : (GFA_BWD_DQ | GFA_BWD_DKV);
   if (stages & ~(GFA_BWD_DQ | GFA_BWD_DKV)) return fail(GFA_ERR_INVALID_ARGUMENT, "unknown stages bits 0x%x", stages);
   const Entry* e = lookup(a->head_dim);
@@ -370,11 +391,12 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   pq.scale = a->scale;
   pq.scale_log2 = scale_log2;
   pq.cap = soft_cap(a->scale, a->softcap);
+  pq.drop = dropout_of(a->dropout_p, a->dropout_seed);
   pq.lse_ld = a->lse_ld;
   pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves / e->dq_split);
   hipError_t err = hipSuccess;
   if (stages & GFA_BWD_DQ) {
-    err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, e->dq_split, bf16, cap, stream);
+    err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, e->dq_split, bf16, cap, drop, stream);
     if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dQ launch failed: %s", hipGetErrorString(err));
   }
   if (!(stages & GFA_BWD_DKV)) return ok();
@@ -408,16 +430,17 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   pk.scale_log2 = scale_log2;
   pk.inv_scale = 1.0f / a->scale;
   pk.cap = pq.cap;
+  pk.drop = pq.drop;
   pk.q_splits = qs;
   pk.lse_ld = a->lse_ld;
   // Soft-capped problems run the plain-chain form: the windowed D=256 pair starts its chains
   // from the row statistics and keeps no raw score. The split count stays the shared rule's
   // (any split is exact), so the workspace size does not depend on the cap.
-  const DkvForm& f = cap ? e->dkv : dkv_form(e, a->causal, a->window, a->seq_len);
+  const DkvForm& f = (cap || drop) ? e->dkv : dkv_form(e, a->causal, a->window, a->seq_len);
   const int keys_per_wg = 32 * (f.waves / f.roles);
   pk.n_kb = (pk.N + keys_per_wg - 1) / keys_per_wg;
   pk.nblocks = (pk.n_kb + 3) / 4 * 4 * pk.B * pk.Hkv * qs;  // key blocks in groups of four (bwd_dkv_kernel)
-  err = gfa::launch_bwd_dkv(pk, a->head_dim, f.bq, f.waves, f.roles, bf16, cap, stream);
+  err = gfa::launch_bwd_dkv(pk, a->head_dim, f.bq, f.waves, f.roles, bf16, cap, drop, stream);
   if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV launch failed: %s", hipGetErrorString(err));
   if (qs > 1) {
     err = gfa::launch_dkv_reduce(pk, a->head_dim, bf16, stream);

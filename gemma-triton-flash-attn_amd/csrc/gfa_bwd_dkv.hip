@@ -40,7 +40,7 @@ namespace gfa {
 // whole-row copies; per-lane loads in the MFMA operand layout touch 32 rows per instruction.
 constexpr bool dkv_stages_rows(int D, int roles) { return roles == 1 && D >= 128; }
 
-template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE, bool CAP>
+template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE, bool CAP, bool DROP>
 __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParams p) {
   constexpr int KT = D / 16;   // MFMA k-steps of the score products (full head dim)
   constexpr int DB = D / 32;   // 32-row blocks of the dV^T / dK^T accumulator
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   constexpr bool INIT = ROLES == 2 && D == 256;
   // CAP (soft-capped scores) needs the raw score, which a chain started from -LSE / scale no
   // longer holds; the host runs soft-capped problems on the other forms.
-  static_assert(!(CAP && INIT), "soft-capping needs the plain score chain");
+  static_assert(!((CAP || DROP) && INIT), "soft-capping and dropout need the plain score chains");
   const int roff0 = l32 * (2 * D) + ((h ^ swz<D>(l32)) << 4);  // tile row l32, chunk h (k-step 0)
   int toff0;  // tiles read transposed (A operands of dV^T, dK^T): rows 4h + t/4, column block 0
   int toffA[4], toffB[4];
@@ -282,6 +282,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   const bool rotate = swa;
   const int phase = rotate && nqt > 0 ? (nqt - qt_lo % nqt) % nqt : 0;
   int r_c = it_lo % p.R;
+  int r_cur = r_c;  // head (within the group) of the tile being processed (the walk runs ahead)
   int qt_c = rotate ? qt_lo + (it_lo / p.R + phase) % max(nqt, 1) : qt_hi - 1 - it_lo / p.R;
   if (it_lo < it_hi) {
     qload.rebase(q_kv + (int64_t)r_c * p.qv.sh, p.qv.sn, p.N);
@@ -350,6 +351,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
         *reinterpret_cast<f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024) = w;
       }
     }
+  };
+  // DROP: is P of query qi (of the tile's head) and this lane's key kept? A dropped entry adds
+  // nothing to dV and its dP counts 0 in dS; a kept one is scaled by 1 / (1 - p).
+  auto kept = [&](int qi) __attribute__((always_inline)) {
+    const int bh = b * p.Hq + kvh * p.R + r_cur;
+    return drop_keep(drop_row(p.drop.seed_lo, p.drop.seed_hi, bh, qi), key, p.drop.thresh);
   };
   // dS = P * (dP - delta) in place of dP. Masked entries have P = 0 and give 0: delta is
   // finite on every row a tile covers (the dQ kernel writes the rows past N of the last
@@ -469,6 +476,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
               const float dpv = RO == 1 ? s[sb][MH + i] : w[i >> 2][i & 3];
               dsv[i] = pv[i] * (dpv - st[0][sb][2 + (i >> 2)][i & 3]);
               if constexpr (CAP) dsv[i] *= gcap[i];
+              if constexpr (DROP) {
+                // dS from the dropped dP; the P this role hands to dV (or keeps) dropped too
+                const bool kp = kept(q0 + sb * 32 + 8 * (2 * RO + (i >> 2)) + 4 * h + (i & 3));
+                dsv[i] = pv[i] * ((kp ? dpv * p.drop.inv_keep : 0.f) - st[0][sb][2 + (i >> 2)][i & 3]);
+                pv[i] = kp ? pv[i] * p.drop.inv_keep : 0.f;
+              }
             }
             // Packed to 16 bits (the accumulations' B operand): the half this role accumulates
             // stays, the half the partner accumulates goes to its slot (role 0: dS, role 1: P).
@@ -512,6 +525,15 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
             }
           }
         }
+        if constexpr (DROP) {
+          if (role == 0) {
+  #pragma unroll
+            for (int sb = 0; sb < SB; ++sb)
+  #pragma unroll
+              for (int r = 0; r < 16; ++r)
+                s[sb][r] = kept(q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) ? s[sb][r] * p.drop.inv_keep : 0.f;
+          }
+        }
         barrier_lds();  // P of this tile is in px
         if (role == 1) {
   #pragma unroll
@@ -519,6 +541,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
             f32x4 pv4[4];
   #pragma unroll
             for (int j = 0; j < 4; ++j) pv4[j] = *reinterpret_cast<const f32x4 GFA_LDS*>(pxr + (sb * 4 + j) * 1024);
+            if constexpr (DROP) {
+  #pragma unroll
+              for (int r = 0; r < 16; ++r)
+                s[sb][r] = kept(q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) ? s[sb][r] * p.drop.inv_keep : 0.f;
+            }
             if constexpr (INIT) {
 #pragma unroll
               for (int r = 0; r < 16; ++r) s[sb][r] *= pv4[r >> 2][r & 3];  // dS = P (dP - delta)
@@ -565,7 +592,20 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       }
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
-      if constexpr (CAP) {
+      if constexpr (DROP) {
+        // dS = P (kept dP / (1 - p) - delta); dV takes the kept P / (1 - p).
+        make_p(s, st[0], q0);
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const bool kp = kept(q0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3));
+            const float pv = s[sb][r];
+            dp[sb][r] = pv * ((kp ? dp[sb][r] * p.drop.inv_keep : 0.f) - st[NS - 1][sb][r >> 2][r & 3]);
+            s[sb][r] = kp ? pv * p.drop.inv_keep : 0.f;
+          }
+        }
+      } else if constexpr (CAP) {
         // P of the capped scores, and dS = P (1 - tanh^2) (dP - delta), element by element.
         const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
 #pragma unroll
@@ -651,6 +691,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     }
     qload.rebase(q_kv + (int64_t)r_n * p.qv.sh, p.qv.sn, p.N);
     dload.rebase(d_kv + (int64_t)r_n * p.dov.sh, p.dov.sn, p.N);
+    r_cur = r_c;
     r_c = r_n;
     qt_c = qt_n;
     tile_step(smem + cur * TILE, smem + (2 + cur) * TILE, smem + (cur ^ 1) * TILE, smem + (2 + (cur ^ 1)) * TILE, px,
@@ -794,50 +835,58 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const BwdDkvParams p, i
 }
 
 // Explicit instantiations of every built variant (device code and host launch stubs).
-#define GFA_DKV_INST(DD, BB, WW, RR, EE, CC)                                              \
-  template __global__ void bwd_dkv_kernel<DD, BB, true, WW, RR, EE, CC>(const BwdDkvParams);  \
-  template __global__ void bwd_dkv_kernel<DD, BB, false, WW, RR, EE, CC>(const BwdDkvParams);
-GFA_DKV_INST(512, 32, 4, 2, 1, false)
-GFA_DKV_INST(256, 32, 4, 1, 1, false)
-GFA_DKV_INST(256, 32, 4, 2, 2, false)
-GFA_DKV_INST(64, 32, 4, 1, 2, false)
-GFA_DKV_INST(128, 32, 4, 2, 2, false)
-// Soft-capped instances (D=256 runs the one-wave form; the windowed pair starts its chains from
-// the row statistics).
-GFA_DKV_INST(512, 32, 4, 2, 1, true)
-GFA_DKV_INST(256, 32, 4, 1, 1, true)
-GFA_DKV_INST(64, 32, 4, 1, 2, true)
-GFA_DKV_INST(128, 32, 4, 2, 2, true)
+#define GFA_DKV_INST(DD, BB, WW, RR, EE, CC, XX)                                                  \
+  template __global__ void bwd_dkv_kernel<DD, BB, true, WW, RR, EE, CC, XX>(const BwdDkvParams);  \
+  template __global__ void bwd_dkv_kernel<DD, BB, false, WW, RR, EE, CC, XX>(const BwdDkvParams);
+GFA_DKV_INST(512, 32, 4, 2, 1, false, false)
+GFA_DKV_INST(256, 32, 4, 1, 1, false, false)
+GFA_DKV_INST(256, 32, 4, 2, 2, false, false)
+GFA_DKV_INST(64, 32, 4, 1, 2, false, false)
+GFA_DKV_INST(128, 32, 4, 2, 2, false, false)
+// Soft-capped and dropout instances (D=256 runs the one-wave form; the windowed pair starts its
+// chains from the row statistics).
+#define GFA_DKV_EXT(CC, XX)                   \
+  GFA_DKV_INST(512, 32, 4, 2, 1, CC, XX)      \
+  GFA_DKV_INST(256, 32, 4, 1, 1, CC, XX)      \
+  GFA_DKV_INST(64, 32, 4, 1, 2, CC, XX)       \
+  GFA_DKV_INST(128, 32, 4, 2, 2, CC, XX)
+GFA_DKV_EXT(true, false)
+GFA_DKV_EXT(false, true)
+#undef GFA_DKV_EXT
 #undef GFA_DKV_INST
 template __global__ void dkv_reduce_kernel<true>(const BwdDkvParams, int);
 template __global__ void dkv_reduce_kernel<false>(const BwdDkvParams, int);
 
-template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE, bool CAP>
+template <int D, int BQ, bool IS_BF16, int NW, int ROLES, int WPE, bool CAP, bool DROP>
 static hipError_t launch_dkv_t(const BwdDkvParams& p, hipStream_t stream) {
   const unsigned stage_bytes = dkv_stages_rows(D, ROLES) ? NW * BQ * D * 2 : 0;  // the kernel's stage_raw
-  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW, ROLES, WPE, CAP>), dim3(p.nblocks), dim3(NW * 64), stage_bytes,
-                     stream, p);
+  hipLaunchKernelGGL((bwd_dkv_kernel<D, BQ, IS_BF16, NW, ROLES, WPE, CAP, DROP>), dim3(p.nblocks), dim3(NW * 64),
+                     stage_bytes, stream, p);
   return hipGetLastError();
 }
 
 // Built dK/dV variants: (head dim, queries per tile, waves per workgroup, waves per 32 keys,
 // waves per SIMD).
-hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, int nw, int roles, bool bf16, bool cap,
+hipError_t launch_bwd_dkv(const BwdDkvParams& p, int D, int bq, int nw, int roles, bool bf16, bool cap, bool drop,
                           hipStream_t stream) {
-#define GFA_DKV_CASE(DD, BB, WW, RR, EE, CC)                                               \
-  if (D == DD && bq == BB && nw == WW && roles == RR && cap == CC) {                       \
-    return bf16 ? launch_dkv_t<DD, BB, true, WW, RR, EE, CC>(p, stream)                    \
-                : launch_dkv_t<DD, BB, false, WW, RR, EE, CC>(p, stream);                  \
+#define GFA_DKV_CASE(DD, BB, WW, RR, EE, CC, XX)                                           \
+  if (D == DD && bq == BB && nw == WW && roles == RR && cap == CC && drop == XX) {         \
+    return bf16 ? launch_dkv_t<DD, BB, true, WW, RR, EE, CC, XX>(p, stream)                \
+                : launch_dkv_t<DD, BB, false, WW, RR, EE, CC, XX>(p, stream);              \
   }
-  GFA_DKV_CASE(512, 32, 4, 2, 1, false)
-  GFA_DKV_CASE(256, 32, 4, 1, 1, false)
-  GFA_DKV_CASE(256, 32, 4, 2, 2, false)
-  GFA_DKV_CASE(64, 32, 4, 1, 2, false)
-  GFA_DKV_CASE(128, 32, 4, 2, 2, false)
-  GFA_DKV_CASE(512, 32, 4, 2, 1, true)
-  GFA_DKV_CASE(256, 32, 4, 1, 1, true)
-  GFA_DKV_CASE(64, 32, 4, 1, 2, true)
-  GFA_DKV_CASE(128, 32, 4, 2, 2, true)
+  GFA_DKV_CASE(512, 32, 4, 2, 1, false, false)
+  GFA_DKV_CASE(256, 32, 4, 1, 1, false, false)
+  GFA_DKV_CASE(256, 32, 4, 2, 2, false, false)
+  GFA_DKV_CASE(64, 32, 4, 1, 2, false, false)
+  GFA_DKV_CASE(128, 32, 4, 2, 2, false, false)
+#define GFA_DKV_EXT(CC, XX)                   \
+  GFA_DKV_CASE(512, 32, 4, 2, 1, CC, XX)      \
+  GFA_DKV_CASE(256, 32, 4, 1, 1, CC, XX)      \
+  GFA_DKV_CASE(64, 32, 4, 1, 2, CC, XX)       \
+  GFA_DKV_CASE(128, 32, 4, 2, 2, CC, XX)
+  GFA_DKV_EXT(true, false)
+  GFA_DKV_EXT(false, true)
+#undef GFA_DKV_EXT
 #undef GFA_DKV_CASE
   return hipErrorInvalidValue;
 }

@@ -27,7 +27,7 @@ namespace gfa {
 // there only adds a barrier and a round trip (measured 0.7% slower).
 constexpr bool dq_stages_rows(int D, int split) { return split == 1 && D >= 128; }
 
-template <int D, int BKV, bool IS_BF16, int NW, int SPLIT, bool CAP>
+template <int D, int BKV, bool IS_BF16, int NW, int SPLIT, bool CAP, bool DROP>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p) {
   constexpr int DH = D / SPLIT;  // head-dim slice of dQ^T one wave accumulates
   constexpr int KT = D / 16;     // k-steps of a score chain (always the full head dim)
@@ -223,19 +223,38 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   // directly and dS = P (dP - delta) costs one multiply (16 AGPRs, which the one-wave-per-SIMD
   // budget has; at D <= 128 they would cost an occupancy step, so the subtraction stays).
   // In a pair only role 1 runs that chain.
-  constexpr bool DP_FROM_DELTA = D >= 256;
+  constexpr bool DP_FROM_DELTA = D >= 256 && !DROP;  // DROP scales dP by the mask first
   f32x16 neg_delta = f32x16{};
   if constexpr (DP_FROM_DELTA) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) neg_delta[r] = dh == SPLIT - 1 ? -delta : 0.f;
   }
-  const float delta_left = DP_FROM_DELTA ? 0.f : delta;  // what dS still subtracts
+  // DROP in a pair: both roles subtract delta from their (dropped) dP half, but only role 1 holds
+  // the dO rows it comes from; it hands delta over through the pair's exchange area (idle until
+  // the first tile step, which starts behind a barrier).
+  float delta_pair = delta;
+  if constexpr (DROP && SPLIT == 2) {
+    float GFA_LDS* const slot = reinterpret_cast<float GFA_LDS*>(xch + (wave >> 1) * XCH) + lane;
+    if (dh == 1) *slot = delta;
+    barrier_lds();
+    delta_pair = *slot;
+  }
+  const float delta_left = DP_FROM_DELTA ? 0.f : delta_pair;  // what dS still subtracts
   if constexpr (DP_FROM_DELTA) pin_agpr(neg_delta);       // the chain's C operand lives there
 
   f32x16 acc[DBH];
 #pragma unroll
   for (int i = 0; i < DBH; ++i) acc[i] = f32x16{};
 
+  // DROP: the row key of this lane's query; dP of a dropped entry is 0, a kept one / (1 - p).
+  const unsigned drow = DROP ? drop_row(p.drop.seed_lo, p.drop.seed_hi, b * p.Hq + head, q) : 0u;
+  auto dp_kept = [&](float dpv, int key) __attribute__((always_inline)) {
+    if constexpr (DROP) {
+      return drop_keep(drow, key, p.drop.thresh) ? dpv * p.drop.inv_keep : 0.f;
+    } else {
+      return dpv;
+    }
+  };
   // P of a raw score, times dS's soft-cap factor 1 - tanh^2 with CAP (so dS = this * (dP - delta)).
   auto p_of = [&](float sv) __attribute__((always_inline)) {
     if constexpr (CAP) {
@@ -295,7 +314,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       for (int i = 0; i < 8; ++i) {
         const float sv = RO == 0 ? own[sb][MH + i] : w[i >> 2][i & 3];
         const float dpv = RO == 1 ? own[sb][MH + i] : w[i >> 2][i & 3];
-        ds[i] = p_of(sv) * (DP_FROM_DELTA ? dpv : dpv - delta_left);
+        const int key = k0 + sb * 32 + 8 * ((MH + i) >> 2) + 4 * h + (i & 3);
+        ds[i] = p_of(sv) * (DP_FROM_DELTA ? dpv : dp_kept(dpv, key) - delta_left);
       }
       if (need_mask) {
 #pragma unroll
@@ -380,7 +400,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float dpd = DP_FROM_DELTA ? dp[sb][r] : dp[sb][r] - delta_left;
+        const float dpd = DP_FROM_DELTA ? dp[sb][r]
+                                        : dp_kept(dp[sb][r], k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) - delta_left;
         s[sb][r] = p_of(s[sb][r]) * dpd;
       }
     }
@@ -469,11 +490,13 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
 
 // Explicit instantiations of every built variant (device code and host launch stubs), plain and
 // soft-capped.
-#define GFA_DQ_INST(DD, SS)                                                          \
-  template __global__ void bwd_dq_kernel<DD, 32, true, 4, SS, false>(const BwdDqParams);  \
-  template __global__ void bwd_dq_kernel<DD, 32, false, 4, SS, false>(const BwdDqParams); \
-  template __global__ void bwd_dq_kernel<DD, 32, true, 4, SS, true>(const BwdDqParams);   \
-  template __global__ void bwd_dq_kernel<DD, 32, false, 4, SS, true>(const BwdDqParams);
+#define GFA_DQ_INST(DD, SS)                                                                 \
+  template __global__ void bwd_dq_kernel<DD, 32, true, 4, SS, false, false>(const BwdDqParams);  \
+  template __global__ void bwd_dq_kernel<DD, 32, false, 4, SS, false, false>(const BwdDqParams); \
+  template __global__ void bwd_dq_kernel<DD, 32, true, 4, SS, true, false>(const BwdDqParams);   \
+  template __global__ void bwd_dq_kernel<DD, 32, false, 4, SS, true, false>(const BwdDqParams);  \
+  template __global__ void bwd_dq_kernel<DD, 32, true, 4, SS, false, true>(const BwdDqParams);   \
+  template __global__ void bwd_dq_kernel<DD, 32, false, 4, SS, false, true>(const BwdDqParams);
 GFA_DQ_INST(512, 2)
 GFA_DQ_INST(256, 1)
 GFA_DQ_INST(128, 1)
@@ -481,28 +504,34 @@ GFA_DQ_INST(64, 1)
 #undef GFA_DQ_INST
 
 template <int D, int BKV, bool IS_BF16, int NW, int SPLIT>
-static hipError_t launch_dq_t(const BwdDqParams& p, bool cap, hipStream_t stream) {
+static hipError_t launch_dq_t(const BwdDqParams& p, bool cap, bool drop, hipStream_t stream) {
   const unsigned stage_bytes = dq_stages_rows(D, SPLIT) ? NW * BKV * D * 2 : 0;  // the kernel's stage_raw
   if (cap) {
-    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, true>), dim3(p.g.nblocks), dim3(NW * 64), stage_bytes,
-                       stream, p);
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, true, false>), dim3(p.g.nblocks), dim3(NW * 64),
+                       stage_bytes, stream, p);
+  } else if (drop) {
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, false, true>), dim3(p.g.nblocks), dim3(NW * 64),
+                       stage_bytes, stream, p);
   } else {
-    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, false>), dim3(p.g.nblocks), dim3(NW * 64), stage_bytes,
-                       stream, p);
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, false, false>), dim3(p.g.nblocks), dim3(NW * 64),
+                       stage_bytes, stream, p);
   }
   return hipGetLastError();
 }
 
 // Built dQ variants: D=512 on wave pairs (head-dim halves), D=256/128/64 one wave per 32 rows.
-hipError_t launch_bwd_dq(const BwdDqParams& p, int D, int bkv, int split, bool bf16, bool cap, hipStream_t stream) {
-  if (D == 512 && bkv == 32 && split == 2)
-    return bf16 ? launch_dq_t<512, 32, true, 4, 2>(p, cap, stream) : launch_dq_t<512, 32, false, 4, 2>(p, cap, stream);
-  if (D == 256 && bkv == 32 && split == 1)
-    return bf16 ? launch_dq_t<256, 32, true, 4, 1>(p, cap, stream) : launch_dq_t<256, 32, false, 4, 1>(p, cap, stream);
-  if (D == 128 && bkv == 32 && split == 1)
-    return bf16 ? launch_dq_t<128, 32, true, 4, 1>(p, cap, stream) : launch_dq_t<128, 32, false, 4, 1>(p, cap, stream);
-  if (D == 64 && bkv == 32 && split == 1)
-    return bf16 ? launch_dq_t<64, 32, true, 4, 1>(p, cap, stream) : launch_dq_t<64, 32, false, 4, 1>(p, cap, stream);
+hipError_t launch_bwd_dq(const BwdDqParams& p, int D, int bkv, int split, bool bf16, bool cap, bool drop,
+                         hipStream_t stream) {
+  if (cap && drop) return hipErrorInvalidValue;  // not built together
+#define GFA_DQ_CASE(DD, SS)                                                                       \
+  if (D == DD && bkv == 32 && split == SS)                                                        \
+    return bf16 ? launch_dq_t<DD, 32, true, 4, SS>(p, cap, drop, stream)                          \
+                : launch_dq_t<DD, 32, false, 4, SS>(p, cap, drop, stream);
+  GFA_DQ_CASE(512, 2)
+  GFA_DQ_CASE(256, 1)
+  GFA_DQ_CASE(128, 1)
+  GFA_DQ_CASE(64, 1)
+#undef GFA_DQ_CASE
   return hipErrorInvalidValue;
 }
 

@@ -61,6 +61,26 @@ __device__ __forceinline__ float from16(short x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Dropout mask: a 32-bit integer mixer (xor-shift / multiply, the "lowbias32" constants) applied
+// twice, first to the row (seed, query head, query row), then to that and the key index. Pure
+// function of the position, so the forward and both backward kernels draw the same mask in
+// their different lane layouts; oracle/attention_oracle.py restates it.
+__device__ __forceinline__ unsigned drop_mix(unsigned x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+// Row key of query row i of query head bh (= b * Hq + h).
+__device__ __forceinline__ unsigned drop_row(unsigned seed_lo, unsigned seed_hi, int bh, int i) {
+  return drop_mix((seed_lo ^ drop_mix(seed_hi + (unsigned)bh * 0x9e3779b9u)) + (unsigned)i);
+}
+__device__ __forceinline__ bool drop_keep(unsigned row, int j, unsigned thresh) {
+  return drop_mix(row ^ ((unsigned)j * 0x85ebca6bu)) >= thresh;
+}
+
 // tanh(x) = 1 - 2 / (exp(2x) + 1): one exp2 and one reciprocal (v_exp_f32, v_rcp_f32),
 // exactly +-1 once exp(2x) overflows or underflows; absolute error about 1e-7.
 __device__ __forceinline__ float cap_tanh(float x) {

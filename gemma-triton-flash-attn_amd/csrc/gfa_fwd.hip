@@ -38,7 +38,7 @@
 
 namespace gfa {
 
-template <int D, int BKV, bool IS_BF16, int NW, int WPE, bool SEG, bool CAP>
+template <int D, int BKV, bool IS_BF16, int NW, int WPE, bool SEG, bool CAP, bool DROP>
 __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   constexpr int KT = D / 16;   // MFMA k-steps over the head dim
   constexpr int DB = D / 32;   // 32-row blocks of the O^T accumulator
@@ -259,13 +259,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
       }
     }
     i16x8 pb[BKV / 16];
+    // DROP: the row sum takes every P, the PV product only the kept ones (1 / (1 - p) is
+    // applied with the normalisation).
+    const unsigned drow = DROP ? drop_row(p.drop.seed_lo, p.drop.seed_hi, b * p.Hq + head, q0 + l32) : 0u;
 #pragma unroll
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float pv = fast_exp2(s[sb][r] * xs - m_ref);
         l_run += pv;
-        pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pv);
+        float pk = pv;
+        if constexpr (DROP) pk = drop_keep(drow, k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3), p.drop.thresh) ? pv : 0.f;
+        pb[sb * 2 + (r >> 3)][r & 7] = to16<IS_BF16>(pk);
       }
     }
     // O^T += V^T P^T with a fixed read-ahead pipeline.
@@ -332,7 +337,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   const int r32 = ln & 31;
   const float l_tot = halves_sum(l_run);
   if (active && q < p.N) {
-    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;  // a row that sees no key (empty segment): O = 0
+    // a row that sees no key (empty segment): O = 0; DROP: kept P scaled by 1 / (1 - p)
+    const float inv = l_tot > 0.f ? (DROP ? p.drop.inv_keep : 1.0f) / l_tot : 0.f;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -353,57 +359,66 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
 
 // Explicit instantiations of every built variant (both the device code and the host
 // launch stubs must exist for each one).
-#define GFA_FWD_INST(DD, BB, WW, EE, CC)                                                  \
-  template __global__ void fwd_kernel<DD, BB, true, WW, EE, false, CC>(const FwdParams);  \
-  template __global__ void fwd_kernel<DD, BB, false, WW, EE, false, CC>(const FwdParams); \
-  template __global__ void fwd_kernel<DD, BB, true, WW, EE, true, CC>(const FwdParams);   \
-  template __global__ void fwd_kernel<DD, BB, false, WW, EE, true, CC>(const FwdParams);
-GFA_FWD_INST(512, 32, 4, 1, false)
-GFA_FWD_INST(256, 64, 4, 1, false)
-GFA_FWD_INST(256, 32, 4, 1, false)
-GFA_FWD_INST(256, 32, 4, 2, false)
-GFA_FWD_INST(128, 64, 4, 2, false)
-GFA_FWD_INST(128, 32, 4, 2, false)
-GFA_FWD_INST(64, 64, 4, 3, false)
-GFA_FWD_INST(64, 32, 4, 3, false)
-// Soft-capped instances: the registry's default tiles only.
-GFA_FWD_INST(512, 32, 4, 1, true)
-GFA_FWD_INST(256, 32, 4, 2, true)
-GFA_FWD_INST(128, 64, 4, 2, true)
-GFA_FWD_INST(128, 32, 4, 2, true)
-GFA_FWD_INST(64, 64, 4, 3, true)
+#define GFA_FWD_INST(DD, BB, WW, EE, CC, XX)                                                  \
+  template __global__ void fwd_kernel<DD, BB, true, WW, EE, false, CC, XX>(const FwdParams);  \
+  template __global__ void fwd_kernel<DD, BB, false, WW, EE, false, CC, XX>(const FwdParams); \
+  template __global__ void fwd_kernel<DD, BB, true, WW, EE, true, CC, XX>(const FwdParams);   \
+  template __global__ void fwd_kernel<DD, BB, false, WW, EE, true, CC, XX>(const FwdParams);
+GFA_FWD_INST(512, 32, 4, 1, false, false)
+GFA_FWD_INST(256, 64, 4, 1, false, false)
+GFA_FWD_INST(256, 32, 4, 1, false, false)
+GFA_FWD_INST(256, 32, 4, 2, false, false)
+GFA_FWD_INST(128, 64, 4, 2, false, false)
+GFA_FWD_INST(128, 32, 4, 2, false, false)
+GFA_FWD_INST(64, 64, 4, 3, false, false)
+GFA_FWD_INST(64, 32, 4, 3, false, false)
+// Soft-capped and dropout instances: the registry's default tiles only.
+#define GFA_FWD_EXT(CC, XX)                  \
+  GFA_FWD_INST(512, 32, 4, 1, CC, XX)        \
+  GFA_FWD_INST(256, 32, 4, 2, CC, XX)        \
+  GFA_FWD_INST(128, 64, 4, 2, CC, XX)        \
+  GFA_FWD_INST(128, 32, 4, 2, CC, XX)        \
+  GFA_FWD_INST(64, 64, 4, 3, CC, XX)
+GFA_FWD_EXT(true, false)
+GFA_FWD_EXT(false, true)
+#undef GFA_FWD_EXT
 #undef GFA_FWD_INST
 
-template <int D, int BKV, bool IS_BF16, int NW, int WPE, bool CAP>
+template <int D, int BKV, bool IS_BF16, int NW, int WPE, bool CAP, bool DROP>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   if (p.seg_lo != nullptr) {
-    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, true, CAP>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream, p);
+    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, true, CAP, DROP>), dim3(p.g.nblocks), dim3(NW * 64), 0,
+                       stream, p);
   } else {
-    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, false, CAP>), dim3(p.g.nblocks), dim3(NW * 64), 0, stream,
-                       p);
+    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, false, CAP, DROP>), dim3(p.g.nblocks), dim3(NW * 64), 0,
+                       stream, p);
   }
   return hipGetLastError();
 }
 
 // Built forward variants: (head dim, keys per tile, waves per workgroup, waves per SIMD).
-hipError_t launch_fwd(const FwdParams& p, int D, int bkv, int nw, bool bf16, bool cap, hipStream_t stream) {
-#define GFA_FWD_CASE(DD, BB, WW, EE, CC)                                                  \
-  if (D == DD && bkv == BB && nw == WW && cap == CC) {                                    \
-    return bf16 ? launch_fwd_t<DD, BB, true, WW, EE, CC>(p, stream)                       \
-                : launch_fwd_t<DD, BB, false, WW, EE, CC>(p, stream);                     \
+hipError_t launch_fwd(const FwdParams& p, int D, int bkv, int nw, bool bf16, bool cap, bool drop, hipStream_t stream) {
+#define GFA_FWD_CASE(DD, BB, WW, EE, CC, XX)                                              \
+  if (D == DD && bkv == BB && nw == WW && cap == CC && drop == XX) {                      \
+    return bf16 ? launch_fwd_t<DD, BB, true, WW, EE, CC, XX>(p, stream)                   \
+                : launch_fwd_t<DD, BB, false, WW, EE, CC, XX>(p, stream);                 \
   }
-  GFA_FWD_CASE(512, 32, 4, 1, false)
-  GFA_FWD_CASE(256, 64, 4, 1, false)
-  GFA_FWD_CASE(256, 32, 4, 2, false)
-  GFA_FWD_CASE(128, 64, 4, 2, false)
-  GFA_FWD_CASE(128, 32, 4, 2, false)
-  GFA_FWD_CASE(64, 64, 4, 3, false)
-  GFA_FWD_CASE(64, 32, 4, 3, false)
-  GFA_FWD_CASE(512, 32, 4, 1, true)
-  GFA_FWD_CASE(256, 32, 4, 2, true)
-  GFA_FWD_CASE(128, 64, 4, 2, true)
-  GFA_FWD_CASE(128, 32, 4, 2, true)
-  GFA_FWD_CASE(64, 64, 4, 3, true)
+  GFA_FWD_CASE(512, 32, 4, 1, false, false)
+  GFA_FWD_CASE(256, 64, 4, 1, false, false)
+  GFA_FWD_CASE(256, 32, 4, 2, false, false)
+  GFA_FWD_CASE(128, 64, 4, 2, false, false)
+  GFA_FWD_CASE(128, 32, 4, 2, false, false)
+  GFA_FWD_CASE(64, 64, 4, 3, false, false)
+  GFA_FWD_CASE(64, 32, 4, 3, false, false)
+#define GFA_FWD_EXT(CC, XX)                   \
+  GFA_FWD_CASE(512, 32, 4, 1, CC, XX)         \
+  GFA_FWD_CASE(256, 32, 4, 2, CC, XX)         \
+  GFA_FWD_CASE(128, 64, 4, 2, CC, XX)         \
+  GFA_FWD_CASE(128, 32, 4, 2, CC, XX)         \
+  GFA_FWD_CASE(64, 64, 4, 3, CC, XX)
+  GFA_FWD_EXT(true, false)
+  GFA_FWD_EXT(false, true)
+#undef GFA_FWD_EXT
 #undef GFA_FWD_CASE
   return hipErrorInvalidValue;
 }

@@ -5,12 +5,12 @@
 
 namespace gfa {
 
-hipError_t launch_fwd(const FwdParams& p, int head_dim, int block_kv, int nwaves, bool bf16, bool cap,
+hipError_t launch_fwd(const FwdParams& p, int head_dim, int block_kv, int nwaves, bool bf16, bool cap, bool drop,
                       hipStream_t stream);
-hipError_t launch_bwd_dq(const BwdDqParams& p, int head_dim, int block_kv, int split, bool bf16, bool cap,
+hipError_t launch_bwd_dq(const BwdDqParams& p, int head_dim, int block_kv, int split, bool bf16, bool cap, bool drop,
                          hipStream_t stream);
 hipError_t launch_bwd_dkv(const BwdDkvParams& p, int head_dim, int block_q, int waves, int roles, bool bf16, bool cap,
-                          hipStream_t stream);
+                          bool drop, hipStream_t stream);
 hipError_t launch_dkv_reduce(const BwdDkvParams& p, int head_dim, bool bf16, hipStream_t stream);
 
 }  // namespace gfa

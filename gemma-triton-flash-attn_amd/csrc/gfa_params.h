@@ -20,6 +20,15 @@ struct SoftCap {
   float cap_log2;  // softcap * log2(e)
 };
 
+// Attention dropout (the kernels' DROP instances): P_ij of query row i (query head bh = b Hq + h)
+// and key j is kept, scaled by 1 / (1 - p), when drop_hash(drop_row(bh, i), j) >= thresh, and
+// zeroed otherwise; the row sums and the LSE use the undropped P.
+struct Dropout {
+  unsigned seed_lo, seed_hi;
+  unsigned thresh;  // round(p * 2^32): keep probability 1 - thresh / 2^32
+  float inv_keep;   // 1 / (1 - p)
+};
+
 // Work decomposition shared by the forward and dQ kernels: a workgroup owns
 // NWAVES (head, 32-query block) pairs of one KV head: `hpw` heads x `qbw` query blocks.
 struct QGrid {
@@ -47,6 +56,7 @@ struct FwdParams {
   int window;        // 0 = no sliding window; only honoured when causal
   float scale_log2;  // softmax scale * log2(e)
   SoftCap cap;       // read by the CAP instances only
+  Dropout drop;      // read by the DROP instances only
   int store_lse;
   int lse_ld;
   QGrid g;
@@ -69,6 +79,7 @@ struct BwdDqParams {
   float scale;       // softmax scale (applied to dQ at the end)
   float scale_log2;  // scale * log2(e)
   SoftCap cap;       // read by the CAP instances only
+  Dropout drop;      // read by the DROP instances only
   int lse_ld;
   QGrid g;
 };
@@ -91,6 +102,7 @@ struct BwdDkvParams {
   float scale, scale_log2;
   float inv_scale;   // 1 / scale
   SoftCap cap;       // read by the CAP instances only
+  Dropout drop;      // read by the DROP instances only
   int q_splits;
   int lse_ld;
   int n_kb;          // number of key blocks (each WKV keys wide)

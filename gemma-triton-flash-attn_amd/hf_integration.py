@@ -72,17 +72,16 @@ def triton_gqa_attention(module, query, key, value, attention_mask, dropout: flo
     (B, N) padding mask, which becomes a segment table, as do packed sequences
     (``cu_seq_lens_*`` or restarting ``position_ids``). Padding tokens' output rows are zero
     (as with transformers' flash-attention path, which drops them). ``softcap`` (Gemma-2's
-    attention logit soft-capping) runs natively; the reference adapter raises for it. A
-    prepared 4-D mask and non-zero dropout raise NotImplementedError: never wrong numerics.
+    attention logit soft-capping) and ``dropout`` (the probability the model passes in
+    training, 0 in eval) run natively; the reference adapter raises for both. A prepared 4-D
+    mask raises NotImplementedError: never wrong numerics.
     """
-    if dropout != 0.0:
-        raise NotImplementedError("triton_gqa_attention does not support dropout")
     segments = _segments_for(query, attention_mask, kwargs)
     scale = scaling if scaling is not None else module.head_dim ** -0.5
     slide = int(sliding_window) if sliding_window else 0
     is_causal = getattr(module, "is_causal", True)
     out = flash_attn_gqa_op(query, key, value, causal=is_causal, slide_size=slide, scale=scale, segments=segments,
-                            softcap=softcap)
+                            softcap=softcap, dropout_p=float(dropout or 0.0))
     return out.transpose(1, 2).contiguous(), None
 
 

@@ -21,8 +21,8 @@ from typing import Optional
 
 import torch
 
-from .attention import (_backward, _check_inputs, _check_segments, _check_softcap, _default_scale, _forward,
-                        _layout_ok, _norm_window, _prep, lse_ld)
+from .attention import (_backward, _check_dropout, _check_inputs, _check_segments, _check_softcap, _default_scale,
+                        _dropout_seed, _forward, _layout_ok, _norm_window, _prep, lse_ld)
 
 
 def _segs(seg_lo, seg_hi):
@@ -42,14 +42,16 @@ def _out_like(t: torch.Tensor) -> torch.Tensor:
 @torch.library.custom_op("gfa::attn_fwd", mutates_args=(), device_types="cuda")
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, window: int,
              scale: float, seg_lo: Optional[torch.Tensor] = None,
-             seg_hi: Optional[torch.Tensor] = None, softcap: float = 0.0) -> tuple[torch.Tensor, torch.Tensor]:
+             seg_hi: Optional[torch.Tensor] = None, softcap: float = 0.0, dropout_p: float = 0.0,
+             dropout_seed: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
     o, lse = _forward(q, k, v, causal, window, scale, store_lse=True, segments=_segs(seg_lo, seg_hi),
-                      softcap=softcap)
+                      softcap=softcap, dropout_p=dropout_p, dropout_seed=dropout_seed)
     return o, lse
 
 
 @attn_fwd.register_fake
-def _attn_fwd_fake(q, k, v, causal, window, scale, seg_lo=None, seg_hi=None, softcap=0.0):
+def _attn_fwd_fake(q, k, v, causal, window, scale, seg_lo=None, seg_hi=None, softcap=0.0, dropout_p=0.0,
+                   dropout_seed=0):
     B, Hq, N, _ = q.shape
     return _out_like(q), q.new_empty((B, Hq, lse_ld(N)), dtype=torch.float32)
 
@@ -57,42 +59,47 @@ def _attn_fwd_fake(q, k, v, causal, window, scale, seg_lo=None, seg_hi=None, sof
 @torch.library.custom_op("gfa::attn_bwd", mutates_args=(), device_types="cuda")
 def attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, lse: torch.Tensor,
              do: torch.Tensor, causal: bool, window: int, scale: float, seg_lo: Optional[torch.Tensor] = None,
-             seg_hi: Optional[torch.Tensor] = None,
-             softcap: float = 0.0) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+             seg_hi: Optional[torch.Tensor] = None, softcap: float = 0.0, dropout_p: float = 0.0,
+             dropout_seed: int = 0) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     dq, dk, dv, _ = _backward(_prep(q), _prep(k), _prep(v), o, lse, do, causal, window, scale,
-                              segments=_segs(seg_lo, seg_hi), softcap=softcap)
+                              segments=_segs(seg_lo, seg_hi), softcap=softcap, dropout_p=dropout_p,
+                              dropout_seed=dropout_seed)
     return dq, dk, dv
 
 
 @attn_bwd.register_fake
-def _attn_bwd_fake(q, k, v, o, lse, do, causal, window, scale, seg_lo=None, seg_hi=None, softcap=0.0):
+def _attn_bwd_fake(q, k, v, o, lse, do, causal, window, scale, seg_lo=None, seg_hi=None, softcap=0.0, dropout_p=0.0,
+                   dropout_seed=0):
     return _out_like(q), _out_like(k), _out_like(v)
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, causal, window, scale, seg_lo, seg_hi, softcap = inputs
+    q, k, v, causal, window, scale, seg_lo, seg_hi, softcap, dropout_p, dropout_seed = inputs
     o, lse = output
     ctx.save_for_backward(q, k, v, o, lse, seg_lo, seg_hi)
     ctx.causal, ctx.window, ctx.scale, ctx.softcap = causal, window, scale, softcap
+    ctx.dropout = (dropout_p, dropout_seed)
     ctx.mark_non_differentiable(lse)
 
 
 def _attn_fwd_backward(ctx, do, _dlse):
     q, k, v, o, lse, seg_lo, seg_hi = ctx.saved_tensors
-    dq, dk, dv = attn_bwd(q, k, v, o, lse, do, ctx.causal, ctx.window, ctx.scale, seg_lo, seg_hi, ctx.softcap)
-    return dq, dk, dv, None, None, None, None, None, None
+    dq, dk, dv = attn_bwd(q, k, v, o, lse, do, ctx.causal, ctx.window, ctx.scale, seg_lo, seg_hi, ctx.softcap,
+                          ctx.dropout[0], ctx.dropout[1])
+    return dq, dk, dv, None, None, None, None, None, None, None, None
 
 
 attn_fwd.register_autograd(_attn_fwd_backward, setup_context=_setup_context)
 
 
-def flash_attn_gqa_op(q, k, v, causal=False, slide_size=0, *, scale=None, segments=None, softcap=None):
+def flash_attn_gqa_op(q, k, v, causal=False, slide_size=0, *, scale=None, segments=None, softcap=None, dropout_p=0.0):
     """``flash_attn_gqa_train`` through the registered op: same arguments, kernels and
     results, and traceable by ``torch.compile`` (no graph break at the attention call)."""
     _check_inputs(q, k, v)
     segments = _check_segments(segments, q)
     window = _norm_window(causal, slide_size, q.shape[2])
     seg_lo, seg_hi = segments if segments is not None else (None, None)
+    dp = _check_dropout(dropout_p)
     o, _ = torch.ops.gfa.attn_fwd(q, k, v, bool(causal), int(window), _default_scale(q.shape[3], scale),
-                                  seg_lo, seg_hi, _check_softcap(softcap))
+                                  seg_lo, seg_hi, _check_softcap(softcap), dp, _dropout_seed() if dp > 0.0 else 0)
     return o

@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define GFA_VERSION 103 /* 1.0.3: optional logit soft-capping (softcap) */
+#define GFA_VERSION 104 /* 1.0.4: optional attention dropout (1.0.3: logit soft-capping) */
 
 typedef enum {
   GFA_DTYPE_FP16 = 0,
@@ -95,6 +95,11 @@ typedef struct {
   float softcap;       /* 0 = off; > 0: every scaled score x = scale q.k becomes softcap tanh(x / softcap)
                           before the mask and softmax (transformers' logit soft-capping; the reference
                           has none). Runs the registry's default tiles (block_kv must be 0 or it). */
+  float dropout_p;     /* 0 = off; in (0, 1): each P_ij is kept with probability 1 - dropout_p and scaled by
+                          1 / (1 - dropout_p), else zeroed (the LSE is that of the undropped P). The mask
+                          is a pure function of (dropout_seed, b, query head, i, j); the backward must get
+                          the same seed. Not combined with softcap. Default tiles only, as softcap. */
+  uint64_t dropout_seed;
 } gfa_fwd_args;
 
 typedef struct {
@@ -125,6 +130,8 @@ typedef struct {
   const int32_t* seg_lo;  /* the forward's segment table, or NULL */
   const int32_t* seg_hi;
   float softcap;          /* the forward's soft-cap (0 = off) */
+  float dropout_p;        /* the forward's dropout probability and seed (0 = off) */
+  uint64_t dropout_seed;
 } gfa_bwd_args;
 
 /* Tile configuration the library uses for one problem (mirrors the Python registry). */

@@ -32,6 +32,17 @@ backward, dS is multiplied by the derivative 1 - tanh^2(z / softcap) before dQ a
 Pinned by tests/test_oracle.py against that transformers function (forward) and torch
 autograd through it in float64 (backward).
 
+Attention dropout (``dropout`` = (p, seed), p in (0, 1); also unsupported by the reference,
+README.md:255-262, hf_integration.py:60-63): P_ij is kept with probability 1 - p and scaled by
+1 / (1 - p), else zeroed, after the softmax (transformers' eager attention applies
+nn.functional.dropout to the probabilities). The LSE is that of the undropped P; the backward
+uses dS = P (M dP / (1 - p) - delta) with delta = rowsum(dO O). The mask M is the engine's
+counter-based one (``dropout_mask``: a 32-bit xor-shift / multiply mixer of (seed, query head,
+query row, key), restated from csrc/gfa_common.h, drop_row / drop_keep), so that the kernels'
+results can be compared element for element. Pinned by tests/test_oracle.py against float64
+torch autograd through softmax(S) * M / (1 - p) @ V with the same mask, and by the mask's
+keep rate.
+
 Two implementations of the same equations:
   * ``forward`` / ``backward``: numpy float64, dense (N x N per head) - small cases and
     golden vectors;
@@ -74,6 +85,40 @@ def _row_mask(mask, segments, b):
     return mask & (j >= lo) & (j < hi)
 
 
+_U32 = 0xFFFFFFFF
+
+
+def _mix32(x):
+    """The engine's 32-bit mixer (uint32 numpy arrays, wrapping arithmetic)."""
+    x = np.atleast_1d(np.asarray(x, dtype=np.uint32))  # arrays wrap silently (scalars would warn)
+    x = x ^ (x >> np.uint32(16))
+    x = x * np.uint32(0x7FEB352D)
+    x = x ^ (x >> np.uint32(15))
+    x = x * np.uint32(0x846CA68B)
+    x = x ^ (x >> np.uint32(16))
+    return x
+
+
+def dropout_mask(seed: int, bh: int, n: int, p: float) -> np.ndarray:
+    """Boolean (N, N) keep-mask of query head bh (= b * Hq + h): entry [i, j] keeps P_ij."""
+    lo, hi = seed & _U32, (seed >> 32) & _U32
+    base = int(_mix32(np.uint32((hi + bh * 0x9E3779B9) & _U32))[0]) ^ lo
+    rows = _mix32((np.arange(n, dtype=np.uint64) + base) & _U32)
+    keys = ((np.arange(n, dtype=np.uint64) * 0x85EBCA6B) & _U32).astype(np.uint32)
+    u = _mix32(rows.astype(np.uint32)[:, None] ^ keys[None, :])
+    p32 = float(np.float32(p))  # the ABI carries p as a float
+    thresh = int(min(p32 * 4294967296.0, 4294967295.0)) if p32 > 0 else 0
+    return u >= np.uint32(thresh)
+
+
+def _drop(dropout, b, h, Hq, n):
+    """(keep-mask, 1 / (1 - p)) of query head h of batch row b, or (None, 1) without dropout."""
+    if dropout is None or not dropout[0]:
+        return None, 1.0
+    p, seed = dropout
+    return dropout_mask(seed, b * Hq + h, n, p), 1.0 / (1.0 - float(np.float32(p)))
+
+
 def _default_scale(d: int, scale):
     return 1.0 / math.sqrt(d) if scale is None else float(scale)
 
@@ -86,7 +131,7 @@ def _capped(s, softcap):
     return softcap * t, 1.0 - t * t
 
 
-def forward(q, k, v, causal=False, window=0, scale=None, segments=None, softcap=0.0):
+def forward(q, k, v, causal=False, window=0, scale=None, segments=None, softcap=0.0, dropout=None):
     """O (B, Hq, N, D) and natural-log LSE (B, Hq, N), float64."""
     q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
     B, Hq, N, D = q.shape
@@ -105,18 +150,22 @@ def forward(q, k, v, causal=False, window=0, scale=None, segments=None, softcap=
             mx = np.where(seen, s.max(axis=1, keepdims=True), 0.0)
             p = np.where(mask, np.exp(s - mx), 0.0)
             l = p.sum(axis=1, keepdims=True)
-            o[b, h] = np.where(seen, p / np.where(seen, l, 1.0), 0.0) @ v[b, g]
+            pn = np.where(seen, p / np.where(seen, l, 1.0), 0.0)
+            m, ik = _drop(dropout, b, h, Hq, N)
+            if m is not None:
+                pn = np.where(m, pn * ik, 0.0)
+            o[b, h] = pn @ v[b, g]
             lse[b, h] = np.where(seen, mx + np.log(np.where(seen, l, 1.0)), -np.inf)[:, 0]
     return o, lse
 
 
-def backward(q, k, v, do, causal=False, window=0, scale=None, segments=None, softcap=0.0):
+def backward(q, k, v, do, causal=False, window=0, scale=None, segments=None, softcap=0.0, dropout=None):
     """dQ, dK, dV (float64) and delta = rowsum(dO * O) for the loss sum(O * dO)."""
     q, k, v, do = (np.asarray(x, dtype=np.float64) for x in (q, k, v, do))
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     sc = _default_scale(D, scale)
-    o, lse = forward(q, k, v, causal, window, scale, segments, softcap)
+    o, lse = forward(q, k, v, causal, window, scale, segments, softcap, dropout)
     base = allowed_mask(N, causal, window)
     dq = np.zeros_like(q)
     dk = np.zeros_like(k)
@@ -129,12 +178,17 @@ def backward(q, k, v, do, causal=False, window=0, scale=None, segments=None, sof
             s, dcap = _capped(sc * (q[b, h] @ k[b, g].T), softcap)
             p = np.where(mask, np.exp(np.where(mask, s - lse[b, h][:, None], 0.0)), 0.0)
             dp = do[b, h] @ v[b, g].T
+            m, ik = _drop(dropout, b, h, Hq, N)
+            pd = p
+            if m is not None:
+                dp = np.where(m, dp * ik, 0.0)
+                pd = np.where(m, p * ik, 0.0)
             ds = p * (dp - delta[b, h][:, None])
             if dcap is not None:
                 ds = ds * dcap
             dq[b, h] = sc * (ds @ k[b, g])
             dk[b, g] += sc * (ds.T @ q[b, h])
-            dv[b, g] += p.T @ do[b, h]
+            dv[b, g] += pd.T @ do[b, h]
     return dq, dk, dv, delta
 
 

@@ -53,6 +53,7 @@ int main(void) {{
   printf("%zu %zu %zu %zu %zu %zu\\n", offsetof(gfa_fwd_args, lse_ld), offsetof(gfa_fwd_args, stream),
          offsetof(gfa_bwd_args, stages), offsetof(gfa_bwd_args, workspace_bytes),
          offsetof(gfa_fwd_args, softcap), offsetof(gfa_bwd_args, softcap));
+  printf("%zu %zu\\n", offsetof(gfa_fwd_args, dropout_seed), offsetof(gfa_bwd_args, dropout_seed));
   return 0;
 }}
 ''')
@@ -62,7 +63,8 @@ int main(void) {{
     sizes = [int(x) for x in out]
     assert sizes[:3] == [ctypes.sizeof(_lib.FwdArgs), ctypes.sizeof(_lib.BwdArgs), ctypes.sizeof(_lib.ConfigInfo)]
     assert sizes[3:] == [_lib.FwdArgs.lse_ld.offset, _lib.FwdArgs.stream.offset, _lib.BwdArgs.stages.offset,
-                         _lib.BwdArgs.workspace_bytes.offset, _lib.FwdArgs.softcap.offset, _lib.BwdArgs.softcap.offset]
+                         _lib.BwdArgs.workspace_bytes.offset, _lib.FwdArgs.softcap.offset, _lib.BwdArgs.softcap.offset,
+                         _lib.FwdArgs.dropout_seed.offset, _lib.BwdArgs.dropout_seed.offset]
 
 
 @pytest.mark.parametrize("shape", [(1, 32, 4, 16384, 512), (1, 16, 8, 16384, 256), (2, 6, 3, 33, 256),
@@ -118,6 +120,9 @@ def _fwd_args(**over):
     (dict(softcap=float("nan")), 1),
     (dict(softcap=-1.0), 1),
     (dict(head_dim=256, block_kv=64, softcap=5.0), 2),  # soft-capping runs the default tiles only
+    (dict(dropout_p=1.0), 1),
+    (dict(dropout_p=-0.1), 1),
+    (dict(dropout_p=0.1, softcap=5.0), 2),  # not built together
     (dict(k_strides=_lib.Strides(8, 8, 4)), 1),  # row stride not a multiple of 8 elements
 ])
 def test_fwd_rejects_bad_arguments(over, status):
@@ -193,8 +198,17 @@ def test_hf_adapter_rejects_unsupported_features():
 
     mod = SimpleNamespace(head_dim=256, is_causal=True)
     q = torch.zeros(1, 2, 4, 256)
-    with pytest.raises(NotImplementedError):
-        gfa.triton_gqa_attention(mod, q, q, q, None, dropout=0.1)
+    with pytest.raises(NotImplementedError):  # a prepared 4-D mask
+        gfa.triton_gqa_attention(mod, q, q, q, torch.zeros(1, 1, 4, 4))
+    from gemma_triton_flash_attn_amd.attention import _check_dropout, _check_softcap
+
+    for bad in (1.0, -0.1, float("nan")):
+        with pytest.raises(ValueError, match="dropout_p"):
+            _check_dropout(bad)
+    assert _check_dropout(None) == 0.0 and _check_dropout(0.25) == 0.25
+    with pytest.raises(ValueError, match="softcap"):
+        _check_softcap(-1.0)
+    assert _check_softcap(None) == 0.0
 
 
 def test_register_into_transformers():

@@ -59,23 +59,29 @@ def test_autograd_registration_and_formula():
         k = torch.empty(1, 1, 64, 512, device="cuda", dtype=torch.bfloat16)
         o, lse = torch.ops.gfa.attn_fwd(q, k, k, True, 16, 0.04)
         ctx = SimpleNamespace(saved_tensors=(q, k, k, o, lse, None, None), causal=True, window=16, scale=0.04,
-                              softcap=0.0)
+                              softcap=0.0, dropout=(0.0, 0))
         grads = _attn_fwd_backward(ctx, torch.empty_like(o), None)
-        assert len(grads) == 9 and grads[3:] == (None,) * 6
+        assert len(grads) == 11 and grads[3:] == (None,) * 8
         assert grads[0].shape == q.shape and grads[1].shape == k.shape and grads[2].shape == k.shape
         # with a segment table (ragged batch): the same formula, the tables passed through
         lo = torch.empty(1, 64, device="cuda", dtype=torch.int32)
         o2, lse2 = torch.ops.gfa.attn_fwd(q, k, k, True, 16, 0.04, lo, lo)
         ctx = SimpleNamespace(saved_tensors=(q, k, k, o2, lse2, lo, lo), causal=True, window=16, scale=0.04,
-                              softcap=0.0)
+                              softcap=0.0, dropout=(0.0, 0))
         grads = _attn_fwd_backward(ctx, torch.empty_like(o2), None)
-        assert len(grads) == 9 and grads[0].shape == q.shape
+        assert len(grads) == 11 and grads[0].shape == q.shape
         # soft-capped: the cap reaches the backward op
         o3, lse3 = torch.ops.gfa.attn_fwd(q, k, k, True, 16, 0.04, None, None, 30.0)
         ctx = SimpleNamespace(saved_tensors=(q, k, k, o3, lse3, None, None), causal=True, window=16, scale=0.04,
-                              softcap=30.0)
+                              softcap=30.0, dropout=(0.0, 0))
         grads = _attn_fwd_backward(ctx, torch.empty_like(o3), None)
-        assert len(grads) == 9 and grads[0].shape == q.shape
+        assert len(grads) == 11 and grads[0].shape == q.shape
+        # dropout: probability and seed reach the backward op
+        o4, lse4 = torch.ops.gfa.attn_fwd(q, k, k, True, 16, 0.04, None, None, 0.0, 0.1, 1234)
+        ctx = SimpleNamespace(saved_tensors=(q, k, k, o4, lse4, None, None), causal=True, window=16, scale=0.04,
+                              softcap=0.0, dropout=(0.1, 1234))
+        grads = _attn_fwd_backward(ctx, torch.empty_like(o4), None)
+        assert len(grads) == 11 and grads[0].shape == q.shape
 
 
 def test_op_entry_validates_like_the_eager_api():

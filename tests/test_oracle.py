@@ -259,3 +259,55 @@ def test_softcap_chunked_matches_dense_and_large_cap_is_no_cap():
     o_big, _ = orc.forward(q, k, v, True, 0, softcap=1e7)
     o_none, _ = orc.forward(q, k, v, True, 0)
     np.testing.assert_allclose(o_big, o_none, atol=1e-9)
+
+
+def _drop_torch64(q, k, v, do, causal, window, p, seed):
+    """float64 torch autograd through softmax(S) * M / (1 - p) @ V with the oracle's mask."""
+    q, k, v = (torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in (q, k, v))
+    B, Hq, n, d = q.shape
+    r = Hq // k.shape[1]
+    ke, ve = k.repeat_interleave(r, 1), v.repeat_interleave(r, 1)
+    allowed = torch.tensor(orc.allowed_mask(n, causal, window))
+    s = (q @ ke.transpose(-1, -2)) * d ** -0.5
+    pr = torch.softmax(s.masked_fill(~allowed, float("-inf")), dim=-1)
+    keep = torch.tensor(np.stack([np.stack([orc.dropout_mask(seed, b * Hq + h, n, p) for h in range(Hq)])
+                                  for b in range(B)]))
+    o = (pr * keep / (1.0 - float(np.float32(p)))) @ ve
+    (o * torch.tensor(do)).sum().backward()
+    return o.detach().numpy(), q.grad.numpy(), k.grad.numpy(), v.grad.numpy()
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D,causal,window,p", [
+    (1, 4, 2, 13, 8, True, 0, 0.25), (2, 6, 2, 17, 8, True, 5, 0.5), (1, 2, 2, 9, 4, False, 0, 0.1)])
+def test_dropout_matches_torch_autograd(B, Hq, Hkv, N, D, causal, window, p):
+    """Dropout (not in the reference): the oracle's forward and gradients equal float64 torch
+    autograd through the same mask, the LSE is the undropped one, and p = 0 is no dropout."""
+    q, k, v, do = (_rand(s, 90 + i) for i, s in enumerate([(B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D),
+                                                           (B, Hq, N, D)]))
+    seed = 0x1234_5678_9ABC_DEF0
+    o_ref, dq_ref, dk_ref, dv_ref = _drop_torch64(q, k, v, do, causal, window, p, seed)
+    o, lse = orc.forward(q, k, v, causal, window, dropout=(p, seed))
+    dq, dk, dv, _ = orc.backward(q, k, v, do, causal, window, dropout=(p, seed))
+    for a, r in ((o, o_ref), (dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
+        np.testing.assert_allclose(a, r, atol=1e-10, rtol=1e-9)
+    _, lse0 = orc.forward(q, k, v, causal, window)
+    np.testing.assert_allclose(lse, lse0, atol=1e-12)
+    o0, _ = orc.forward(q, k, v, causal, window, dropout=(0.0, seed))
+    np.testing.assert_allclose(o0, orc.forward(q, k, v, causal, window)[0], atol=0)
+
+
+def test_dropout_mask_rate_and_independence():
+    """Keep rate 1 - p (to a few standard errors), per row and per column alike; different
+    heads and seeds give different masks."""
+    n = 512
+    for p in (0.1, 0.5):
+        m = orc.dropout_mask(7, 3, n, p)
+        rate = m.mean()
+        assert abs(rate - (1 - p)) < 4 * np.sqrt(p * (1 - p) / m.size)
+        rows, cols = m.mean(axis=1), m.mean(axis=0)
+        tol = 6 * np.sqrt(p * (1 - p) / n)
+        assert np.abs(rows - (1 - p)).max() < tol and np.abs(cols - (1 - p)).max() < tol
+    a = orc.dropout_mask(7, 3, 256, 0.5)
+    assert (a != orc.dropout_mask(7, 4, 256, 0.5)).mean() > 0.4
+    assert (a != orc.dropout_mask(8, 3, 256, 0.5)).mean() > 0.4
+    assert (a != orc.dropout_mask(7 + (1 << 32), 3, 256, 0.5)).mean() > 0.4
