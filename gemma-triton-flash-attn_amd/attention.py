@@ -235,9 +235,10 @@ def _default_scale(d: int, scale: float | None) -> float:
 class FlashAttnGQAFunction(torch.autograd.Function):
     """Autograd function of the GQA flash attention (reference attention.py:1433-1622).
 
-    forward(q, k, v, causal, slide_size, scale=None, segments=None, softcap=None) -> O; saves
-    q, k, v, O, the fp32 LSE and the segment tables. backward(dO) -> dQ, dK, dV via gfa_bwd (dQ
-    kernel with fused delta, then pack-GQA dKV).
+    forward(q, k, v, causal, slide_size, scale=None, segments=None, softcap=None, dropout_p=0.0)
+    -> O; saves q, k, v, O, the fp32 LSE (of the undropped probabilities), the segment tables and
+    the dropout seed drawn for this call. backward(dO) -> dQ, dK, dV via gfa_bwd (dQ kernel with
+    fused delta, then pack-GQA dKV), regenerating the same dropout mask from that seed.
     """
 
     @staticmethod
