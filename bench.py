@@ -43,9 +43,25 @@ WORKLOADS = {
     "d256_swa1024_gqa2_n16k": dict(B=1, Hq=16, Hkv=8, N=16384, D=256, causal=True, window=1024, dtype="bf16", amp=1.0),
     "c2_d512_causal_gqa8_n8k": dict(B=1, Hq=32, Hkv=4, N=8192, D=512, causal=True, window=0, dtype="bf16", amp=1.0),
     "c4_d512_causal_gqa8_n32k": dict(B=1, Hq=16, Hkv=2, N=32768, D=512, causal=True, window=0, dtype="fp16", amp=0.5),
+    # the headline and config-3 shapes in fp16, the dtype of the reference's published figures
+    "d512_causal_gqa8_n16k_fp16": dict(B=1, Hq=32, Hkv=4, N=16384, D=512, causal=True, window=0, dtype="fp16",
+                                       amp=1.0),
+    "d256_swa1024_gqa2_n16k_fp16": dict(B=1, Hq=16, Hkv=8, N=16384, D=256, causal=True, window=1024, dtype="fp16",
+                                        amp=1.0),
     # the rest of the reference's documented head-dim range (64-512): not Gemma-4 layers
     "d128_causal_gqa4_n16k": dict(B=1, Hq=32, Hkv=8, N=16384, D=128, causal=True, window=0, dtype="bf16", amp=1.0),
     "d64_causal_mha_n16k": dict(B=1, Hq=32, Hkv=32, N=16384, D=64, causal=True, window=0, dtype="bf16", amp=1.0),
+}
+
+
+# The reference's published H100 fp16 times of the same shapes (ms): D=512 causal 32:4 N=16384
+# (/root/reference/benchmarks/attn_only_all_n.json:200-210) and D=256 W=1024 16:8 N=16384
+# (/root/reference/benchmarks/moe_attn_sweep.json:47-57). Reported beside the fp16 rows only.
+REFERENCE_H100_FP16_MS = {
+    "d512_causal_gqa8_n16k_fp16": {"ms_fwd": 47.58, "ms_fwd_bwd": 262.98,
+                                   "source": "benchmarks/attn_only_all_n.json:200-210"},
+    "d256_swa1024_gqa2_n16k_fp16": {"ms_fwd": 0.854, "ms_fwd_bwd": 4.003,
+                                    "source": "benchmarks/moe_attn_sweep.json:47-57"},
 }
 
 
@@ -179,6 +195,9 @@ def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd", 
                           for kname, ms in per.items()}
         print(f"[bench] {name}: kernels " + ", ".join(f"{k_} {v_['ms']:.3f} ms {v_['tflops']:.1f} TF"
                                                      for k_, v_ in res["kernels"].items()), file=sys.stderr, flush=True)
+    ref = REFERENCE_H100_FP16_MS.get(name)
+    if ref is not None:
+        res["reference_h100_fp16"] = dict(ref, speedup_fwd=ref["ms_fwd"] / ms_fwd, speedup_fwd_bwd=ref["ms_fwd_bwd"] / ms_fb)
     del q, k, v, do, qg, kg, vg
     torch.cuda.empty_cache()
     return res
@@ -442,7 +461,7 @@ def main(argv=None):
     ap.add_argument("--no-kernels", action="store_true", help="skip per-kernel timing")
     ap.add_argument("--workloads",
                     default="d512_causal_gqa8_n16k,d256_swa1024_gqa2_n16k,c2_d512_causal_gqa8_n8k,"
-                            "c4_d512_causal_gqa8_n32k",
+                            "c4_d512_causal_gqa8_n32k,d512_causal_gqa8_n16k_fp16,d256_swa1024_gqa2_n16k_fp16",
                     help="comma list of workloads to time (the first one must be the headline)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc passes that measure HBM traffic per kernel")

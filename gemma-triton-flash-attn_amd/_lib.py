@@ -30,6 +30,11 @@ STATUS_NAMES = {
     4: "GFA_ERR_LAUNCH",
 }
 
+# GFA_VERSION of include/gfa.h whose struct layouts FwdArgs / BwdArgs below mirror. A library
+# built from other sources reads another prefix of the argument structs (an older one ignores the
+# segment, soft-cap and dropout fields), so load() refuses it instead of computing wrong results.
+ABI_VERSION = 104
+
 EXPORTED = ("gfa_fwd", "gfa_bwd", "gfa_bwd_noalloc", "gfa_bwd_workspace_size", "gfa_config", "gfa_last_error",
             "gfa_version")
 NOALLOC_SCRATCH_BYTES = 64 << 20  # GFA_NOALLOC_SCRATCH_BYTES
@@ -120,6 +125,11 @@ def load() -> ctypes.CDLL:
         lib.gfa_last_error.restype = ctypes.c_char_p
         lib.gfa_version.argtypes = []
         lib.gfa_version.restype = ctypes.c_int
+        built = int(lib.gfa_version())
+        if built != ABI_VERSION:
+            raise RuntimeError(
+                f"{LIB_PATH} reports GFA_VERSION {built}, but this binding mirrors version {ABI_VERSION}; "
+                "rebuild it with `python gemma-triton-flash-attn_amd/build.py` (or __graft_entry__.build())")
         _lib = lib
         return lib
 

@@ -31,6 +31,7 @@ import math
 import torch
 
 from . import _lib
+from . import segments as _seglib
 from .registry import lookup
 
 _DTYPES = {torch.float16: _lib.GFA_DTYPE_FP16, torch.bfloat16: _lib.GFA_DTYPE_BF16}
@@ -83,7 +84,11 @@ def _check_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
 
 
 def _check_segments(segments, q: torch.Tensor):
-    """(lo, hi) int32 tables of shape (B, N) on q's device, made contiguous; None passes."""
+    """(lo, hi) int32 tables of shape (B, N) on q's device, made contiguous; None passes.
+    Tables that segments.py did not build are checked to partition each row into segments and
+    padding (segments.validate; one device-to-host read, skipped under torch.compile): the
+    kernels read a block's range from its first and last token's bounds, so a malformed table
+    would give wrong results without an error."""
     if segments is None:
         return None
     if len(segments) != 2:
@@ -96,6 +101,8 @@ def _check_segments(segments, q: torch.Tensor):
         if t.device != q.device:
             raise ValueError("segment tables must be on q's device")
         out.append(t.to(torch.int32).contiguous())
+    if not isinstance(segments, _seglib.SegmentTables) and _seglib._host_checks():
+        _seglib.validate(out[0], out[1])
     return tuple(out)
 
 
@@ -138,6 +145,14 @@ def _check_dropout(p) -> float:
     if not math.isfinite(c) or c < 0.0 or c >= 1.0:
         raise ValueError(f"dropout_p={p} must be in [0, 1)")
     return c
+
+
+def _check_cap_and_dropout(softcap: float, dropout_p: float) -> None:
+    """Soft-capping and dropout each run natively, but no kernel instance combines them: raise
+    NotImplementedError (the adapter contract's error for unsupported features, reference
+    hf_integration.py:60-63) before anything is launched."""
+    if softcap > 0.0 and dropout_p > 0.0:
+        raise NotImplementedError("softcap together with dropout_p > 0 is not built (each is supported alone)")
 
 
 def _dropout_seed() -> int:
@@ -249,6 +264,7 @@ class FlashAttnGQAFunction(torch.autograd.Function):
         sc = _default_scale(q.shape[3], scale)
         cap = _check_softcap(softcap)
         dp = _check_dropout(dropout_p)
+        _check_cap_and_dropout(cap, dp)
         seed = _dropout_seed() if dp > 0.0 else 0
         o, lse = _forward(q, k, v, causal, slide_size, sc, store_lse=True, segments=segments, softcap=cap,
                           dropout_p=dp, dropout_seed=seed)

@@ -366,7 +366,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   template __global__ void fwd_kernel<DD, BB, false, WW, EE, true, CC, XX>(const FwdParams);
 GFA_FWD_INST(512, 32, 4, 1, false, false)
 GFA_FWD_INST(256, 64, 4, 1, false, false)
-GFA_FWD_INST(256, 32, 4, 1, false, false)
 GFA_FWD_INST(256, 32, 4, 2, false, false)
 GFA_FWD_INST(128, 64, 4, 2, false, false)
 GFA_FWD_INST(128, 32, 4, 2, false, false)

@@ -37,11 +37,17 @@ def _segments_for(query, attention_mask, kwargs):
       arguments): one row of packed sequences;
     * ``position_ids`` that restart inside a row (packing without a mask, which transformers
       detects the same way).
-    Anything else the kernels cannot express raises NotImplementedError."""
+    Anything else the kernels cannot express raises NotImplementedError.
+
+    Under torch.compile nothing here reads device values on the host (such a read would break
+    the graph): the cu_seq_lens equality check is skipped, and position ids always become a
+    table. For ids without a restart that table is one segment per row, so the results equal the
+    eager path's, which passes no table then."""
     B, _, N, _ = query.shape
+    host = seglib._host_checks()
     cu_q, cu_k = kwargs.get("cu_seq_lens_q"), kwargs.get("cu_seq_lens_k")
     if cu_q is not None or cu_k is not None:
-        if cu_q is None or cu_k is None or not torch.equal(cu_q.to(cu_k.device), cu_k):
+        if cu_q is None or cu_k is None or (host and not torch.equal(cu_q.to(cu_k.device), cu_k)):
             raise NotImplementedError("packed sequences need equal cu_seq_lens_q and cu_seq_lens_k")
         if B != 1:
             raise NotImplementedError("packed sequences (cu_seq_lens) are one row of tokens")
@@ -56,7 +62,7 @@ def _segments_for(query, attention_mask, kwargs):
         except ValueError as e:
             raise NotImplementedError(str(e)) from None
     pos = kwargs.get("position_ids")
-    if pos is not None and pos.dim() == 2 and pos.shape[-1] == N and seglib.is_packed(pos):
+    if pos is not None and pos.dim() == 2 and pos.shape[-1] == N and (not host or seglib.is_packed(pos)):
         return seglib.from_position_ids(pos.to(query.device).expand(B, N))
     return None
 
@@ -93,11 +99,13 @@ def padding_mask_for_engine(batch_size, q_length, kv_length, q_offset=0, kv_offs
     of their own (masking_utils._preprocess_mask_arguments), which would make padded
     batches silently wrong. This one hands the adapter the (B, kv_length) boolean padding
     mask when any key is padded, and None otherwise (the kernels build the causal and
-    window masks themselves)."""
+    window masks themselves). Under torch.compile the mask is handed over as it is (testing
+    it would read a device value on the host); an unpadded mask becomes one segment per row,
+    with the same results."""
     if attention_mask is None:
         return None
     m = attention_mask[:, -kv_length:]
-    if m.shape[1] == kv_length and bool(m.all()):
+    if m.shape[1] == kv_length and seglib._host_checks() and bool(m.all()):
         return None
     return m
 

@@ -48,7 +48,9 @@ Two implementations of the same equations:
     golden vectors;
   * ``forward_chunked`` / ``backward_chunked``: torch float32 on any device, query-chunked
     so N = 32K fits - the large-shape check on the GPU box (a torch fp32 reference of the
-    same op, never the engine).
+    same op, never the engine). They take segments, soft-capping and dropout as well (the
+    mask rows of a chunk from ``dropout_mask_rows``), and are pinned to the dense path with
+    each of them.
 
 Pinned by tests/test_oracle.py against: torch's scaled_dot_product_attention (math
 backend, float64) and its autograd for forward/backward, the committed golden vectors in
@@ -211,9 +213,41 @@ def _chunk_mask(torch, q_lo, q_hi, n, causal, window, device, segments=None, b=0
     return m
 
 
-def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024, segments=None, softcap=0.0):
+def _mix32_t(x):
+    """``_mix32`` on int64 torch tensors holding uint32 values, exact: each product keeps its
+    low 32 bits from two partial products below 2^49, so nothing overflows int64."""
+    m = 0xFFFFFFFF
+
+    def mul(a, c):
+        return (a * (c & 0xFFFF) + (((a * (c >> 16)) & 0xFFFF) << 16)) & m
+
+    x = x ^ (x >> 16)
+    x = mul(x, 0x7FEB352D)
+    x = x ^ (x >> 15)
+    x = mul(x, 0x846CA68B)
+    x = x ^ (x >> 16)
+    return x
+
+
+def dropout_mask_rows(seed: int, bh: int, q_lo: int, q_hi: int, n: int, p: float, device=None):
+    """Rows [q_lo, q_hi) of ``dropout_mask`` as a torch bool tensor on ``device`` (the chunked
+    path's form of the same mask: identical entries, pinned by tests/test_oracle.py)."""
+    import torch
+
+    lo, hi = seed & _U32, (seed >> 32) & _U32
+    base = int(_mix32(np.uint32((hi + bh * 0x9E3779B9) & _U32))[0]) ^ lo
+    rows = _mix32_t((torch.arange(q_lo, q_hi, device=device, dtype=torch.int64) + base) & _U32)
+    keys = (torch.arange(n, device=device, dtype=torch.int64) * 0x85EBCA6B) & _U32
+    u = _mix32_t(rows[:, None] ^ keys[None, :])
+    p32 = float(np.float32(p))
+    thresh = int(min(p32 * 4294967296.0, 4294967295.0)) if p32 > 0 else 0
+    return u >= thresh
+
+
+def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024, segments=None, softcap=0.0,
+                    dropout=None):
     """torch fp32 O and LSE for (B, H, N, D) tensors of any float dtype / device.
-    ``segments``: (lo, hi) integer tensors (B, N), as in ``forward``."""
+    ``segments``: (lo, hi) integer tensors (B, N); ``dropout``: (p, seed); both as in ``forward``."""
     import torch
 
     B, Hq, N, D = q.shape
@@ -240,21 +274,25 @@ def forward_chunked(q, k, v, causal=False, window=0, scale=None, chunk=1024, seg
                     p = torch.exp(s - m)
                     l = p.sum(dim=1, keepdim=True)
                     l1 = torch.where(seen, l, torch.ones_like(l))
+                    if dropout is not None and dropout[0]:
+                        keep = dropout_mask_rows(dropout[1], b * Hq + h, lo, hi, N, dropout[0], q.device)
+                        p = torch.where(keep, p * (1.0 / (1.0 - float(np.float32(dropout[0])))), 0.0)
                     o[b, h, lo:hi] = torch.where(seen, (p @ vf) / l1, torch.zeros_like(qf[lo:hi]))
                     lse[b, h, lo:hi] = torch.where(seen, m + torch.log(l1), torch.full_like(l, float("-inf")))[:, 0]
     return o, lse
 
 
 def backward_chunked(q, k, v, do, causal=False, window=0, scale=None, chunk=1024, o=None, lse=None,
-                     segments=None, softcap=0.0):
-    """torch fp32 dQ, dK, dV, delta. ``o``/``lse`` may be passed to skip the recomputation."""
+                     segments=None, softcap=0.0, dropout=None):
+    """torch fp32 dQ, dK, dV, delta. ``o``/``lse`` may be passed to skip the recomputation
+    (with ``dropout`` they must be the dropped forward's)."""
     import torch
 
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     sc = _default_scale(D, scale)
     if o is None or lse is None:
-        o, lse = forward_chunked(q, k, v, causal, window, scale, chunk, segments, softcap)
+        o, lse = forward_chunked(q, k, v, causal, window, scale, chunk, segments, softcap, dropout)
     dq = torch.empty((B, Hq, N, D), dtype=torch.float32, device=q.device)
     dk = torch.zeros((B, Hkv, N, D), dtype=torch.float32, device=q.device)
     dv = torch.zeros((B, Hkv, N, D), dtype=torch.float32, device=q.device)
@@ -277,10 +315,16 @@ def backward_chunked(q, k, v, do, causal=False, window=0, scale=None, chunk=1024
                         s = softcap * t
                     p = torch.exp((s - lse[b, h, lo:hi, None].float()).masked_fill(~mask, 0.0)).masked_fill(~mask, 0.0)
                     dp = dof[lo:hi] @ vt
+                    pd = p
+                    if dropout is not None and dropout[0]:
+                        keep = dropout_mask_rows(dropout[1], b * Hq + h, lo, hi, N, dropout[0], q.device)
+                        ik = 1.0 / (1.0 - float(np.float32(dropout[0])))
+                        dp = torch.where(keep, dp * ik, 0.0)
+                        pd = torch.where(keep, p * ik, 0.0)
                     ds = p * (dp - delta[b, h, lo:hi, None])
                     if softcap:
                         ds = ds * (1.0 - t * t)
                     dq[b, h, lo:hi] = (ds @ kf) * sc
                     dk[b, g] += (ds.t().contiguous() @ qf[lo:hi]) * sc
-                    dv[b, g] += p.t().contiguous() @ dof[lo:hi]
+                    dv[b, g] += pd.t().contiguous() @ dof[lo:hi]
     return dq, dk, dv, delta

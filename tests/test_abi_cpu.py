@@ -39,6 +39,18 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert lib.gfa_version() == int(re.search(r"#define GFA_VERSION (\d+)", text).group(1))
+    assert _lib.ABI_VERSION == lib.gfa_version()
+
+
+def test_loader_refuses_a_library_of_another_abi_version(monkeypatch):
+    """A libgfa.so whose GFA_VERSION differs from the layout the ctypes structs mirror would read
+    another prefix of the argument structs; load() raises instead."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "ABI_VERSION", _lib.ABI_VERSION - 1)
+    with pytest.raises(RuntimeError, match="GFA_VERSION"):
+        _lib.load()
+    monkeypatch.undo()
+    assert _lib.load().gfa_version() == _lib.ABI_VERSION
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")

@@ -137,3 +137,35 @@ def test_hf_adapter_dropout(device):
     torch.manual_seed(5)
     o_ref, _ = orc.forward(_np(q), _np(k), _np(v), True, 0, dropout=(0.2, _dropout_seed()))
     assert float(np.abs(_np(out.transpose(1, 2)) - o_ref).max()) <= O_TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("D,window,kind", [(512, 0, "left_padded"), (512, 0, "packed"), (256, 40, "left_padded"),
+                                           (256, 40, "packed"), (128, 24, "packed")])
+def test_dropout_with_segments(D, window, kind, device):
+    """Dropout on a padded or packed batch: the SEG+DROP forward instances and the segment paths of
+    both backward kernels, against the oracle with the same segments and mask."""
+    import gemma_triton_flash_attn_amd as gfa
+    from gemma_triton_flash_attn_amd.attention import _backward, _forward
+
+    print(f"dropout+segments case D={D} window={window} {kind}", flush=True)
+    if kind == "left_padded":
+        B, N = 2, 130
+        segs = gfa.segments.from_lengths([N - 37, N - 5], N, left_padding=True, device=device)
+    else:
+        B, N = 1, 150
+        segs = gfa.segments.from_cu_seqlens([0, 40, 41, 97, 140], N, device=device)
+    q, k, v, do = make_inputs(B, 4, 2, N, D, torch.bfloat16, device, seed=D + N)
+    sc = D ** -0.5
+    o, lse = _forward(q, k, v, True, window, sc, store_lse=True, segments=segs, dropout_p=0.2, dropout_seed=SEED)
+    dq, dk, dv, _ = _backward(q, k, v, o, lse, do, True, window, sc, segments=segs, dropout_p=0.2,
+                              dropout_seed=SEED)
+    torch.cuda.synchronize()
+    seg_np = (segs[0].cpu().numpy(), segs[1].cpu().numpy())
+    o_ref, _ = orc.forward(_np(q), _np(k), _np(v), True, window, segments=seg_np, dropout=(0.2, SEED))
+    dq_ref, dk_ref, dv_ref, _ = orc.backward(_np(q), _np(k), _np(v), _np(do), True, window, segments=seg_np,
+                                             dropout=(0.2, SEED))
+    err_o = float(np.abs(_np(o) - o_ref).max())
+    errs = [_rel(_np(g), r) for g, r in ((dq, dq_ref), (dk, dk_ref), (dv, dv_ref))]
+    print(f"  O max-abs {err_o:.3e}  dQ/dK/dV rel {errs[0]:.3e} {errs[1]:.3e} {errs[2]:.3e}", flush=True)
+    assert err_o <= O_TOL[torch.bfloat16]
+    assert max(errs) <= GRAD_TOL

@@ -189,6 +189,44 @@ def test_chunked_matches_dense(causal, window):
         np.testing.assert_allclose(b.numpy(), a, atol=2e-5, rtol=1e-4)
 
 
+@pytest.mark.parametrize("causal,window,segmented", [(True, 0, False), (True, 6, True), (False, 0, False),
+                                                     (False, 0, True)])
+def test_chunked_dropout_matches_dense(causal, window, segmented):
+    """The chunked torch path with dropout (the large-size check on the GPU box) equals the dense
+    float64 path, which test_dropout_matches_torch_autograd pins to torch autograd: same mask
+    rows per chunk (a wrong row offset or head index in the chunked mask fails), same scaling,
+    undropped LSE; also together with a packed segment table."""
+    B, Hq, Hkv, N, D = 2, 4, 2, 37, 8
+    q, k, v, do = (_rand(s, 40 + i) for i, s in enumerate([(B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D), (B, Hq, N, D)]))
+    drop = (0.3, 0x0123_4567_89AB_CDEF)
+    segs = None
+    if segmented:
+        lo = np.array([[0] * 10 + [10] * 20 + list(range(30, 37)), [0] * 37])
+        hi = np.array([[10] * 10 + [30] * 20 + list(range(30, 37)), [37] * 37])
+        segs = (lo, hi)
+    o, lse = orc.forward(q, k, v, causal, window, segments=segs, dropout=drop)
+    dq, dk, dv, delta = orc.backward(q, k, v, do, causal, window, segments=segs, dropout=drop)
+    tq, tk, tv, tdo = (torch.tensor(x, dtype=torch.float32) for x in (q, k, v, do))
+    tsegs = None if segs is None else tuple(torch.tensor(x) for x in segs)
+    o2, lse2 = orc.forward_chunked(tq, tk, tv, causal, window, chunk=8, segments=tsegs, dropout=drop)
+    dq2, dk2, dv2, delta2 = orc.backward_chunked(tq, tk, tv, tdo, causal, window, chunk=8, segments=tsegs,
+                                                 dropout=drop)
+    for a, b in ((o, o2), (lse, lse2), (dq, dq2), (dk, dk2), (dv, dv2), (delta, delta2)):
+        np.testing.assert_allclose(b.numpy(), a, atol=2e-5, rtol=1e-4)
+    # the undropped result is far away (the mask is applied)
+    o0, _ = orc.forward(q, k, v, causal, window, segments=segs)
+    assert np.abs(o0 - o).max() > 0.1
+
+
+def test_chunked_dropout_mask_equals_dense_mask():
+    """``dropout_mask_rows`` (int64 torch arithmetic) equals the numpy uint32 mask entry for entry,
+    for every row slice, including seeds and heads that exercise the high mixer bits."""
+    for seed, bh, n, p in ((7, 3, 300, 0.1), (0xFFFF_FFFF_FFFF_FFFF, 1000, 129, 0.5), (1 << 40, 0, 64, 0.9)):
+        dense = orc.dropout_mask(seed, bh, n, p)
+        for lo, hi in ((0, n), (5, 37), (n - 1, n)):
+            np.testing.assert_array_equal(orc.dropout_mask_rows(seed, bh, lo, hi, n, p).numpy(), dense[lo:hi])
+
+
 @pytest.mark.parametrize("causal,window", [(True, 0), (True, 7), (True, 1), (False, 0), (True, 64)])
 def test_cpu_baseline_restatement_matches_oracle(causal, window):
     """The function the reported CPU baseline times (oracle/cpu_baseline.py sdpa_math_gqa,

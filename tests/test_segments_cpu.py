@@ -63,6 +63,55 @@ def test_from_cu_seqlens_and_position_ids_agree():
         seg.from_cu_seqlens([0, 11], 10)
 
 
+def test_from_cu_seqlens_without_sequences_is_all_padding():
+    """cu_seqlens = [0] (no sequence): every token is padding, with no indexing past the
+    one-element tensor (torch.where evaluates both of its branches)."""
+    lo, hi = seg.from_cu_seqlens([0], 8)
+    assert lo.tolist() == [list(range(8))] and hi.tolist() == [list(range(8))]
+    with pytest.raises(ValueError):
+        seg.from_cu_seqlens([], 8)
+    seg.validate(lo, hi)
+
+
+def test_builders_return_tables_that_validate():
+    """Every builder's output is a SegmentTables (taken as well-formed by the entry points) and
+    passes the partition check that user-supplied tables get."""
+    m = torch.tensor([[1, 1, 1, 0, 0], [0, 0, 1, 1, 1], [1, 1, 1, 1, 1], [0, 0, 0, 0, 0]], dtype=torch.bool)
+    built = [seg.from_padding_mask(m), seg.from_lengths([3, 5], 5), seg.from_cu_seqlens([0, 3, 7, 8], 10),
+             seg.from_position_ids(torch.tensor([[0, 1, 2, 0, 1, 2, 3, 0, 0, 0]]))]
+    for t in built:
+        assert isinstance(t, seg.SegmentTables)
+        seg.validate(*t)
+    for name in ROWS:
+        _, _, (lo, hi) = _build(name)
+        seg.validate(torch.as_tensor(lo), torch.as_tensor(hi))
+
+
+@pytest.mark.parametrize("lo,hi,why", [
+    ([[0, 0, 2, 2]], [[2, 1, 4, 4]], "hi below the token"),
+    ([[0, 0, 0, 0]], [[4, 4, 4, 5]], "hi past N"),
+    ([[0, 0, 2, 3]], [[2, 2, 4, 4]], "a member that neither continues nor starts a segment"),
+    ([[0, 0, 1, 1]], [[2, 2, 4, 4]], "a segment starting inside the previous one"),
+    ([[0, 0, 0, 0]], [[3, 3, 4, 4]], "hi changing inside a segment"),
+    ([[1, 1, 1, 1]], [[4, 4, 4, 4]], "a segment that starts before its first token"),
+    ([[0, 0, 2, 0]], [[2, 2, 3, 4]], "lo decreasing"),
+    ([[0, 5, 2, 3]], [[1, 5, 3, 4]], "a padding token with lo = hi away from itself"),
+])
+def test_malformed_user_tables_raise(lo, hi, why):
+    """Tables that do not partition the row would make the kernels' tile-range trimming (from a
+    block's first and last token) wrong without an error; they are rejected before any launch."""
+    lo, hi = torch.tensor(lo, dtype=torch.int32), torch.tensor(hi, dtype=torch.int32)
+    with pytest.raises(ValueError, match="partition"):
+        seg.validate(lo, hi)
+    from gemma_triton_flash_attn_amd.attention import _check_segments
+
+    q = torch.empty(1, 2, lo.shape[1], 64)
+    with pytest.raises(ValueError, match="partition"):
+        _check_segments((lo, hi), q)
+    # the same tensors wrapped as builder output are trusted (no device read)
+    assert _check_segments(seg.SegmentTables(lo, hi), q) is not None
+
+
 ROWS = {
     # name: N, list of per-row runs (start, end, is_segment)
     "right_left_full_empty": (13, [[(0, 9, True), (9, 10, False), (10, 11, False), (11, 12, False), (12, 13, False)],
