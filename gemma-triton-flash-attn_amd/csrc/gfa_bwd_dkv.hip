@@ -66,8 +66,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   constexpr bool PRIO = WPE >= 2;
   static_assert(!STAGE_PAIR || NW == 4, "one tile buffer per wave");
 
-  __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NU * PX];
+  // Shared form: the row statistics of a tile (LSE then delta of its BQ rows) travel into LDS with
+  // the tile, double buffered, so no VGPRs hold them across the score chain.
+  constexpr int STB = SHARED ? 512 : 0;
+  static_assert(!SHARED || BQ <= 64, "a statistics block holds 64 rows of LSE and of delta");
+  __shared__ __attribute__((aligned(1024))) char smem_raw[4 * TILE + NU * PX + 2 * STB];
   char GFA_LDS* smem = (char GFA_LDS*)smem_raw;
+  char GFA_LDS* const stat_lds = smem + 4 * TILE + NU * PX;
   // STAGE: each wave's TILE-byte block of this launch-sized array takes its V rows before the
   // loop and its dV, then dK rows after it (its K rows go to one of the tile buffers). Dynamic,
   // so the compiler's occupancy estimate (static LDS only) stays that of the tile buffers.
@@ -284,11 +289,24 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   int r_c = it_lo % p.R;
   int r_cur = r_c;  // head (within the group) of the tile being processed (the walk runs ahead)
   int qt_c = rotate ? qt_lo + (it_lo / p.R + phase) % max(nqt, 1) : qt_hi - 1 - it_lo / p.R;
+  // Shared form: wave 0 copies the LSE rows, wave 1 the delta rows of head r, query tile qt into a
+  // statistics block, 64 rows from the tile's first (one dword per lane; the tile uses BQ of them,
+  // rows past the buffer's end read as zeros). Whole-wave copies keep the buffer resource
+  // wave-uniform: under a lane-dependent branch the compiler rebuilt it from VGPRs every step.
+  auto copy_stats = [&](int r, int qt, char GFA_LDS* dst) __attribute__((always_inline)) {
+    if (wave < 2) {
+      const float* base = (wave == 0 ? stat_kv0 : stat_kv1) + (int64_t)r * p.lse_ld;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, p.lse_ld * 4, 0x00020000);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void GFA_LDS*)(dst + wave * 256), 4, lane * 4, qt * BQ * 4, 0, 0);
+    }
+  };
   if (it_lo < it_hi) {
     qload.rebase(q_kv + (int64_t)r_c * p.qv.sh, p.qv.sn, p.N);
     dload.rebase(d_kv + (int64_t)r_c * p.dov.sh, p.dov.sn, p.N);
     qload.load(qt_c * BQ, smem);
     dload.load(qt_c * BQ, smem + 2 * TILE);
+    if constexpr (SHARED) copy_stats(r_c, qt_c, stat_lds);
   }
 
   // P on the key lanes (rows = queries per register): exp2 against the row LSE, masked.
@@ -385,10 +403,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // does not wait for the prefetch before reading the current tile.
   auto tile_step = [&](const char GFA_LDS* __restrict__ qt, const char GFA_LDS* __restrict__ dt,
                        char GFA_LDS* __restrict__ qn, char GFA_LDS* __restrict__ dn, char GFA_LDS* __restrict__ pxr,
-                       int row_n, int q0, const f32x4 (&st)[NS][SB][4]) __attribute__((always_inline)) {
+                       const char GFA_LDS* __restrict__ stc, char GFA_LDS* __restrict__ stn, int r_n, int row_n, int q0,
+                       const f32x4 (&st)[NS][SB][4]) __attribute__((always_inline)) {
     // The copies of the next tile are spread over the score chains, one every few MFMAs (a
     // run of copy issues would hold up the in-order MFMA stream).
     constexpr int NI = TileLoader<D, BQ, NW>::NI;  // copy instructions per tile and wave
+    if constexpr (SHARED) copy_stats(r_n, row_n / BQ, stn);
     if constexpr (ROLES == 2) {
       // role 0: S = Q K^T from the Q tile, then dV^T += dO^T P reads the dO tile transposed.
       // role 1: dP = dO V^T from the dO tile, then dK^T += Q^T dS reads the Q tile transposed.
@@ -410,13 +430,19 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
         if (sb == 0) {
-          s[sb] = chain_ld(std::integral_constant<int, 2 * NI>{}, ct, sf[0], [&](int i) {
+          auto ld = [&](int i) {
             if (i < NI) {
               qload.load_part(i, row_n, qn);
             } else {
               dload.load_part(i - NI, row_n, dn);
             }
-          }, c0[sb]);
+          };
+          if constexpr (SHARED) {
+            // the chain in VGPRs (the AGPRs hold dV^T / dK^T; see mma32_vgpr)
+            s[sb] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, 2 * NI>(ct, roff, sf[0], ld);
+          } else {
+            s[sb] = chain_ld(std::integral_constant<int, 2 * NI>{}, ct, sf[0], ld, c0[sb]);
+          }
         } else {
           s[sb] = chain(ct, sb * 32 * (2 * D), sf[0], c0[sb]);
         }
@@ -435,6 +461,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
         // with P computed by role 0 alone, role 1 sat out about 20% of each step.
         const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
         auto slot = [&](int sb, int k, int j) __attribute__((always_inline)) { return pxr + (sb * 4 + k) * 2048 + j * 1024; };
+        // this role's rows of the statistics block: LSE of rows 16 role + 8 j + 4 h + 0..3, then delta
+        f32x4 stl[SB][4];
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int off = (sb * 32 + 16 * role + 8 * j + 4 * h) * 4;
+            stl[sb][j] = *reinterpret_cast<const f32x4 GFA_LDS*>(stc + off);
+            stl[sb][2 + j] = *reinterpret_cast<const f32x4 GFA_LDS*>(stc + 256 + off);
+          }
         auto shared = [&](auto ro) __attribute__((always_inline)) {
           constexpr int RO = decltype(ro)::value;
           constexpr int MH = 8 * RO, OH = 8 * (1 - RO);
@@ -458,11 +494,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
               const float sv = RO == 0 ? s[sb][MH + i] : w[i >> 2][i & 3];
               if constexpr (CAP) {
                 const float t = cap_tanh(sv * p.cap.cap_a);
-                pv[i] = fast_exp2(t * p.cap.cap_log2 - st[0][sb][i >> 2][i & 3] * kLog2e);
+                pv[i] = fast_exp2(t * p.cap.cap_log2 - stl[sb][i >> 2][i & 3] * kLog2e);
                 gcap[i] = 1.f - t * t;
                 continue;
               }
-              pv[i] = fast_exp2(sv * p.scale_log2 - st[0][sb][i >> 2][i & 3] * kLog2e);
+              pv[i] = fast_exp2(sv * p.scale_log2 - stl[sb][i >> 2][i & 3] * kLog2e);
             }
             if (need_mask) {
   #pragma unroll
@@ -474,12 +510,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   #pragma unroll
             for (int i = 0; i < 8; ++i) {
               const float dpv = RO == 1 ? s[sb][MH + i] : w[i >> 2][i & 3];
-              dsv[i] = pv[i] * (dpv - st[0][sb][2 + (i >> 2)][i & 3]);
+              dsv[i] = pv[i] * (dpv - stl[sb][2 + (i >> 2)][i & 3]);
               if constexpr (CAP) dsv[i] *= gcap[i];
               if constexpr (DROP) {
                 // dS from the dropped dP; the P this role hands to dV (or keeps) dropped too
                 const bool kp = kept(q0 + sb * 32 + 8 * (2 * RO + (i >> 2)) + 4 * h + (i & 3));
-                dsv[i] = pv[i] * ((kp ? dpv * p.drop.inv_keep : 0.f) - st[0][sb][2 + (i >> 2)][i & 3]);
+                dsv[i] = pv[i] * ((kp ? dpv * p.drop.inv_keep : 0.f) - stl[sb][2 + (i >> 2)][i & 3]);
                 pv[i] = kp ? pv[i] * p.drop.inv_keep : 0.f;
               }
             }
@@ -658,15 +694,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     // multiple of 64), issued before the prefetch so they are not queued behind it.
     f32x4 st[NS][SB][4];
     if constexpr (SHARED) {
-      // each role's half of the rows (registers 8 role .. 8 role + 7): LSE, then delta
-      const int64_t roff = (int64_t)r_c * p.lse_ld + q0 + 4 * h + 16 * role;
-#pragma unroll
-      for (int sb = 0; sb < SB; ++sb)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          st[0][sb][j] = *reinterpret_cast<const f32x4*>(stat_kv0 + roff + sb * 32 + 8 * j);
-          st[0][sb][2 + j] = *reinterpret_cast<const f32x4*>(stat_kv1 + roff + sb * 32 + 8 * j);
-        }
+      // shared form: the statistics come from LDS (copied with the tile), read after the chain
     } else
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
@@ -695,7 +723,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     r_c = r_n;
     qt_c = qt_n;
     tile_step(smem + cur * TILE, smem + (2 + cur) * TILE, smem + (cur ^ 1) * TILE, smem + (2 + (cur ^ 1)) * TILE, px,
-              qt_n * BQ, q0, st);
+              stat_lds + cur * STB, stat_lds + (cur ^ 1) * STB, r_n, qt_n * BQ, q0, st);
   }
   drain_tile_copies();
 

@@ -223,7 +223,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   // directly and dS = P (dP - delta) costs one multiply (16 AGPRs, which the one-wave-per-SIMD
   // budget has; at D <= 128 they would cost an occupancy step, so the subtraction stays).
   // In a pair only role 1 runs that chain.
-  constexpr bool DP_FROM_DELTA = D >= 256 && !DROP;  // DROP scales dP by the mask first
+  // One wave per 32 rows: the S^T and dP^T chains accumulate in VGPRs through inline-asm MFMAs
+  // (mma32_vgpr), so the dS work reads them without AGPR moves (32 per tile, in the phase that is
+  // vector-bound); a VGPR chain cannot start from the AGPR-held -delta, so dS subtracts it.
+  constexpr bool VCHAIN = SPLIT == 1 && SB == 1;
+  constexpr bool DP_FROM_DELTA = D >= 256 && !DROP && !VCHAIN;  // DROP scales dP by the mask first
   f32x16 neg_delta = f32x16{};
   if constexpr (DP_FROM_DELTA) {
 #pragma unroll
@@ -351,7 +355,12 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     // straight-line body keeps the accumulators resident in registers.
     f32x16 s[SB], dp[SB];
     i16x8 dsb[BKV / 16];  // dS^T, packed 16-bit: the B operand of dQ^T += K^T dS^T
-    if constexpr (SPLIT == 1) {
+    if constexpr (VCHAIN) {
+      s[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(kt, koff, qf, [&](int i) { kload.load_part(i, rn, kn); });
+      __builtin_amdgcn_sched_barrier(0);
+      dp[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(vt, koff, df, [&](int i) { vload.load_part(i, rn, vn); });
+      __builtin_amdgcn_sched_barrier(0);
+    } else if constexpr (SPLIT == 1) {
       s[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, NI>(kt, koff, 0, qf, [&](int i) { kload.load_part(i, rn, kn); });
       __builtin_amdgcn_sched_barrier(0);
       dp[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, NI>(vt, koff, 0, df, [&](int i) { vload.load_part(i, rn, vn); },

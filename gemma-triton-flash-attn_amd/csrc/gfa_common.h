@@ -406,6 +406,85 @@ __device__ __forceinline__ f32x16 mma_chain1_lds_ld_b(const char GFA_LDS* tile, 
   return c;
 }
 
+// One 32x32x16 MFMA into a VGPR accumulator, as inline assembly: in a kernel whose fp32
+// accumulators are pinned to AGPRs (asm "a" constraints) the compiler selects the AGPR form for
+// every MFMA, so a score chain built from the builtin runs in AGPRs, and with the AGPR file full
+// it moves an accumulator block out to VGPRs and back around every chain. FIRST: the chain's
+// first product (C = 0). The destination is early-clobber so that it never overlaps an input.
+// Dependent products back to back on one accumulator need no wait states; the caller pads the
+// chain's end before the result is read (mfma_result_fence).
+template <bool IS_BF16, bool FIRST>
+__device__ __forceinline__ void mma32_vgpr(f32x16& c, const i16x8& a, const i16x8& b) {
+  if constexpr (FIRST) {
+    if constexpr (IS_BF16) {
+      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+    } else {
+      asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+    }
+  } else {
+    if constexpr (IS_BF16) {
+      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    } else {
+      asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    }
+  }
+}
+// The compiler cannot see the pass count of an MFMA written in inline assembly, so it inserts no
+// wait states before the first read of its result. An 8-pass XDL op on gfx950 needs 12 before a
+// VALU, LDS or memory instruction reads its VGPR result; 16 are inserted here.
+__device__ __forceinline__ void mfma_result_fence(f32x16& c) { asm volatile("s_nop 7\n\ts_nop 7" : "+v"(c)); }
+
+// mma_chain1_lds_ld with the chain accumulating in VGPRs (mma32_vgpr), started from zero.
+template <bool IS_BF16, int KT, int PF, int NL, typename LD>
+__device__ __forceinline__ f32x16 mma_chain1_lds_ld_vgpr(const char GFA_LDS* tile, const int (&koff)[8],
+                                                         const i16x8 (&bf)[KT], LD&& ld) {
+  static_assert(PF <= KT && NL >= 1 && KT % NL == 0, "bad chain shape");
+  constexpr int EV = KT / NL;
+  f32x16 c;
+  i16x8 a[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, koff[i & 7] + 256 * (i >> 3));
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const i16x8 cur = a[kk % PF];
+    if (kk + PF < KT) a[kk % PF] = lds_read16(tile, koff[(kk + PF) & 7] + 256 * ((kk + PF) >> 3));
+    if (kk == 0) {
+      mma32_vgpr<IS_BF16, true>(c, cur, bf[kk]);
+    } else {
+      mma32_vgpr<IS_BF16, false>(c, cur, bf[kk]);
+    }
+    if (kk % EV == 0) ld(kk / EV);
+  }
+  mfma_result_fence(c);
+  return c;
+}
+
+// mma_chain1_lds_ld_b with the chain accumulating in VGPRs (mma32_vgpr), started from zero.
+template <bool IS_BF16, int KT, int PF, int NL, typename LD>
+__device__ __forceinline__ f32x16 mma_chain1_lds_ld_b_vgpr(const char GFA_LDS* tile, int koff0, const i16x8 (&bf)[KT],
+                                                           LD&& ld) {
+  static_assert(PF <= KT && NL >= 1 && KT % NL == 0, "bad chain shape");
+  constexpr int EV = KT / NL;
+  const int kb = opaque(koff0);
+  f32x16 c;
+  i16x8 a[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) a[i] = lds_read16(tile, kstep_off(kb, i));
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const i16x8 cur = a[kk % PF];
+    if (kk + PF < KT) a[kk % PF] = lds_read16(tile, kstep_off(kb, kk + PF));
+    if (kk == 0) {
+      mma32_vgpr<IS_BF16, true>(c, cur, bf[kk]);
+    } else {
+      mma32_vgpr<IS_BF16, false>(c, cur, bf[kk]);
+    }
+    if (kk % EV == 0) ld(kk / EV);
+  }
+  mfma_result_fence(c);
+  return c;
+}
+
 // mma_chain1_lds with NL tile-copy instructions ld(0..NL-1) spread over the chain, one after
 // every KT / NL MFMAs. A wave issues in order and the copies of all its workgroup's waves
 // share the CU's texture path (each copy instruction moves 1 KB), so a run of copy issues

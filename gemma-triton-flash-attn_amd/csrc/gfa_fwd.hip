@@ -183,6 +183,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   // D=256; at D=512 (one wave per SIMD, the max hidden under the chain) 1% slower. fp16's margin
   // (2^15) is within reach of a long row's sum, so fp16 keeps the per-tile max and check.
   constexpr bool LAZY = IS_BF16 && D <= 256;
+  // One wave per SIMD with O^T pinned in AGPRs: the S^T chain accumulates in VGPRs through
+  // inline-asm MFMAs (mma32_vgpr); built from the builtin it runs in AGPRs, and the softmax then
+  // reads its scores back with AGPR moves.
+  constexpr bool VCHAIN = WPE == 1 && SB == 1;
   auto step = [&](auto mode, int t, const char GFA_LDS* kt, const char GFA_LDS* vt, char GFA_LDS* kn,
                   char GFA_LDS* vn) __attribute__((always_inline)) {
     constexpr int MODE = decltype(mode)::value;  // 0: accumulate; 1: row max only
@@ -196,13 +200,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     const int rn = rot(min(t + 1, t_hi - 1)) * BKV;
     const int k0 = rot(t) * BKV;
     f32x16 s[SB];
-    s[0] = mma_chain1_lds_ld_b<IS_BF16, KT, PF, 2 * NI>(kt, koff0, 0, qf, [&](int i) {
+    auto ld = [&](int i) {
       if (i < NI) {
         kload.load_part(i, rn, kn);
       } else {
         vload.load_part(i - NI, rn, vn);
       }
-    });
+    };
+    if constexpr (VCHAIN) {
+      s[0] = mma_chain1_lds_ld_b_vgpr<IS_BF16, KT, PF, 2 * NI>(kt, koff0, qf, ld);
+    } else {
+      s[0] = mma_chain1_lds_ld_b<IS_BF16, KT, PF, 2 * NI>(kt, koff0, 0, qf, ld);
+    }
 #pragma unroll
     for (int sb = 1; sb < SB; ++sb) s[sb] = mma_chain1_lds_b<IS_BF16, KT, 4>(kt, koff0, sb * 32 * (2 * D), qf);
     __builtin_amdgcn_sched_barrier(0);
