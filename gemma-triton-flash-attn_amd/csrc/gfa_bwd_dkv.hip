@@ -208,6 +208,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // each read, where eight-entry offset tables would cost 14 registers (5% faster measured).
   // The other head dims keep the tables (measured 2-4% faster there).
   constexpr bool ONE_BASE = D == 128 || (D == 256 && WPE == 2);
+  // One wave per 32 keys at D >= 256 (both accumulators fill the AGPRs): the two score chains
+  // accumulate in VGPRs (mma32_vgpr), so no accumulator block is moved out and back around them.
+  constexpr bool VCHAIN1 = ROLES == 1 && SB == 1 && D >= 256 && !ONE_BASE;
   // Role pairs at two waves per SIMD and D=256 (register-bound): the score chains start from
   // the row statistic instead of zero, so neither LSE nor delta stays live past the chain:
   // role 0 from -LSE / scale (P = exp2(scale * log2e * acc)), role 1 from -delta (dS = P acc).
@@ -612,7 +615,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
         if (sb == 0) {
-          s[sb] = chain_ld(std::integral_constant<int, NI>{}, qt, sf[0], [&](int i) { qload.load_part(i, row_n, qn); });
+          auto ldq = [&](int i) { qload.load_part(i, row_n, qn); };
+          if constexpr (VCHAIN1) {
+            s[sb] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(qt, roff, sf[0], ldq);
+          } else {
+            s[sb] = chain_ld(std::integral_constant<int, NI>{}, qt, sf[0], ldq);
+          }
         } else {
           s[sb] = chain(qt, sb * 32 * (2 * D), sf[0]);
         }
@@ -621,7 +629,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
 #pragma unroll
       for (int sb = 0; sb < SB; ++sb) {
         if (sb == 0) {
-          dp[sb] = chain_ld(std::integral_constant<int, NI>{}, dt, sf[1], [&](int i) { dload.load_part(i, row_n, dn); });
+          auto ldd = [&](int i) { dload.load_part(i, row_n, dn); };
+          if constexpr (VCHAIN1) {
+            dp[sb] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(dt, roff, sf[1], ldd);
+          } else {
+            dp[sb] = chain_ld(std::integral_constant<int, NI>{}, dt, sf[1], ldd);
+          }
         } else {
           dp[sb] = chain(dt, sb * 32 * (2 * D), sf[1]);
         }

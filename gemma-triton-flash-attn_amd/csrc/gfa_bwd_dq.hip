@@ -223,21 +223,22 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   // directly and dS = P (dP - delta) costs one multiply (16 AGPRs, which the one-wave-per-SIMD
   // budget has; at D <= 128 they would cost an occupancy step, so the subtraction stays).
   // In a pair only role 1 runs that chain.
-  // One wave per 32 rows: the S^T and dP^T chains accumulate in VGPRs through inline-asm MFMAs
-  // (mma32_vgpr), so the dS work reads them without AGPR moves (32 per tile, in the phase that is
-  // vector-bound); a VGPR chain cannot start from the AGPR-held -delta, so dS subtracts it.
-  constexpr bool VCHAIN = SPLIT == 1 && SB == 1;
+  // The S^T and dP^T chains accumulate in VGPRs through inline-asm MFMAs (mma32_vgpr), so the dS
+  // work and the pair's exchange read them without AGPR moves (16-32 per tile); a VGPR chain
+  // cannot start from the AGPR-held -delta, so dS subtracts it (in a pair, role 1 hands delta
+  // to role 0 once).
+  constexpr bool VCHAIN = SB == 1;
   constexpr bool DP_FROM_DELTA = D >= 256 && !DROP && !VCHAIN;  // DROP scales dP by the mask first
   f32x16 neg_delta = f32x16{};
   if constexpr (DP_FROM_DELTA) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) neg_delta[r] = dh == SPLIT - 1 ? -delta : 0.f;
   }
-  // DROP in a pair: both roles subtract delta from their (dropped) dP half, but only role 1 holds
-  // the dO rows it comes from; it hands delta over through the pair's exchange area (idle until
-  // the first tile step, which starts behind a barrier).
+  // A pair that subtracts delta in dS (DROP, VCHAIN): both roles subtract it from their dP half,
+  // but only role 1 holds the dO rows it comes from; it hands delta over through the pair's
+  // exchange area (idle until the first tile step, which starts behind a barrier).
   float delta_pair = delta;
-  if constexpr (DROP && SPLIT == 2) {
+  if constexpr (SPLIT == 2 && !DP_FROM_DELTA) {
     float GFA_LDS* const slot = reinterpret_cast<float GFA_LDS*>(xch + (wave >> 1) * XCH) + lane;
     if (dh == 1) *slot = delta;
     barrier_lds();
@@ -355,7 +356,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
     // straight-line body keeps the accumulators resident in registers.
     f32x16 s[SB], dp[SB];
     i16x8 dsb[BKV / 16];  // dS^T, packed 16-bit: the B operand of dQ^T += K^T dS^T
-    if constexpr (VCHAIN) {
+    if constexpr (VCHAIN && SPLIT == 1) {
       s[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(kt, koff, qf, [&](int i) { kload.load_part(i, rn, kn); });
       __builtin_amdgcn_sched_barrier(0);
       dp[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(vt, koff, df, [&](int i) { vload.load_part(i, rn, vn); });
@@ -380,13 +381,18 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       // 2.5x slower).
       f32x16 own[SB];
       auto run = [&](const char GFA_LDS* ct, const f32x16& init) __attribute__((always_inline)) {
-        own[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, 2 * NI>(ct, koff, 0, qf, [&](int i) {
+        auto ld = [&](int i) {
           if (i < NI) {
             kload.load_part(i, rn, kn);
           } else {
             vload.load_part(i - NI, rn, vn);
           }
-        }, init);
+        };
+        if constexpr (VCHAIN) {
+          own[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, 2 * NI>(ct, koff, qf, ld);
+        } else {
+          own[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, 2 * NI>(ct, koff, 0, qf, ld, init);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int sb = 1; sb < SB; ++sb) own[sb] = mma_chain1_lds<IS_BF16, KT, 4>(ct, koff, sb * 32 * (2 * D), qf) + init;
