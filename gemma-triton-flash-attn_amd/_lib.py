@@ -33,10 +33,10 @@ STATUS_NAMES = {
 # GFA_VERSION of include/gfa.h whose struct layouts FwdArgs / BwdArgs below mirror. A library
 # built from other sources reads another prefix of the argument structs (an older one ignores the
 # segment, soft-cap and dropout fields), so load() refuses it instead of computing wrong results.
-ABI_VERSION = 104
+ABI_VERSION = 105
 
 EXPORTED = ("gfa_fwd", "gfa_bwd", "gfa_bwd_noalloc", "gfa_bwd_workspace_size", "gfa_config", "gfa_last_error",
-            "gfa_version")
+            "gfa_version", "gfa_set_runtime_scheduling")
 NOALLOC_SCRATCH_BYTES = 64 << 20  # GFA_NOALLOC_SCRATCH_BYTES
 
 
@@ -125,6 +125,8 @@ def load() -> ctypes.CDLL:
         lib.gfa_last_error.restype = ctypes.c_char_p
         lib.gfa_version.argtypes = []
         lib.gfa_version.restype = ctypes.c_int
+        lib.gfa_set_runtime_scheduling.argtypes = [ctypes.c_int32]
+        lib.gfa_set_runtime_scheduling.restype = ctypes.c_int
         built = int(lib.gfa_version())
         if built != ABI_VERSION:
             raise RuntimeError(
@@ -138,6 +140,12 @@ def check(status: int) -> None:
     if status != 0:
         msg = load().gfa_last_error().decode(errors="replace")
         raise GfaError(status, msg)
+
+
+def set_runtime_scheduling(enable: bool) -> bool:
+    """Switch the run-time work distribution of the head_dim-512 grids on or off (process-wide;
+    results are bitwise the same either way). Returns the previous setting."""
+    return bool(load().gfa_set_runtime_scheduling(1 if enable else 0))
 
 
 def strides_of(t) -> Strides:

@@ -2,6 +2,7 @@
 // decomposition and kernel dispatch. Nothing here allocates, frees or synchronises.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -205,11 +206,102 @@ int check_dims(int B, int Hq, int Hkv, int N, int D, int dtype, int window) {
   return GFA_OK;
 }
 
+// ---------------------------------------------------------------------------------
+// Run-time work hand-out (gfa::WorkQueue) for the D=512 forward and dQ grids. Their blocks carry
+// unequal work (causal rows) and last 0.1-7 ms, and with one workgroup per CU the hardware's
+// in-order dispatch leaves CUs idle while the next block waits for a CU on a busy shader engine;
+// the eight XCDs also run at clocks up to 10% apart, and a static grid gives each the same share.
+// A persistent grid of one workgroup per CU takes the blocks from per-XCD queues instead
+// (gfa::WorkFetch): 1-2% off the forward and 2-3% off dQ at 8k-32k tokens. The dK/dV grid keeps
+// the hardware's dispatch: the same hand-out made it 3-4% slower, with or without taking blocks
+// from other XCDs' queues.
+// The queue counters live in a library-owned device array of slots, handed out round-robin, one
+// per launch; each launch first zeroes its slot with a one-workgroup kernel on the same stream (a
+// kernel, not a memset, so that graph capture records an ordinary kernel node). A slot is reused
+// after kWqSlots further launches on the device, which only a caller keeping that many launches
+// in flight on other streams at once could overlap. Every GPU holds its own copy of the array;
+// in host code `wq_pool` only names the symbol, whose address hipGetSymbolAddress gives per device.
+// ---------------------------------------------------------------------------------
+constexpr int kWqSlots = 256;
+constexpr int kWqStride = 16;  // counters per slot (8 used), 64 bytes
+static __device__ __align__(256) unsigned wq_pool[kWqSlots * kWqStride];
+
+__global__ void wq_reset_kernel(unsigned* c) {
+  if (threadIdx.x < kWqStride) c[threadIdx.x] = 0u;
+}
+
+struct WqDevice {
+  std::atomic<unsigned*> base{nullptr};  // published after cus (release / acquire)
+  int cus = 0;
+  std::atomic<unsigned> next{0};
+};
+constexpr int kMaxWqDevices = 64;
+std::mutex g_wq_mu;
+WqDevice g_wq[kMaxWqDevices];
+
+// The grids that take their blocks at run time: the forward and dQ kernels at D=512 (one
+// workgroup per CU), unless switched off (gfa_set_runtime_scheduling).
+std::atomic<int> g_runtime_scheduling{1};
+bool dynamic_grid(int head_dim) { return head_dim == 512 && g_runtime_scheduling.load(std::memory_order_relaxed) != 0; }
+
+// Fills `q` for a launch of `nblocks` static blocks on `stream`: the static grid, or a persistent
+// grid of one workgroup per CU with a freshly zeroed counter slot.
+int setup_queue(hipStream_t stream, int head_dim, int nblocks, gfa::WorkQueue* q) {
+  q->wq = nullptr;
+  q->grid = nblocks;
+  if (!dynamic_grid(head_dim)) return GFA_OK;
+  int dev = -1;
+  hipError_t err = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "cannot resolve the stream's device: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxWqDevices) return GFA_OK;  // untracked device: the static grid
+  WqDevice& d = g_wq[dev];
+  unsigned* base = d.base.load(std::memory_order_acquire);
+  if (base == nullptr) {
+    std::lock_guard<std::mutex> lock(g_wq_mu);
+    base = d.base.load(std::memory_order_relaxed);
+    if (base == nullptr) {
+      int cur = -1;
+      if ((err = hipGetDevice(&cur)) != hipSuccess)
+        return fail(GFA_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(err));
+      if (cur != dev && (err = hipSetDevice(dev)) != hipSuccess)
+        return fail(GFA_ERR_LAUNCH, "hipSetDevice(%d) failed: %s", dev, hipGetErrorString(err));
+      void* p = nullptr;
+      int cus = 0;
+      err = hipGetSymbolAddress(&p, HIP_SYMBOL(wq_pool));
+      hipError_t err2 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      const hipError_t restore = cur != dev ? hipSetDevice(cur) : hipSuccess;  // the caller's device again
+      if (err != hipSuccess || p == nullptr)
+        return fail(GFA_ERR_LAUNCH, "hipGetSymbolAddress(wq_pool) failed on device %d: %s", dev, hipGetErrorString(err));
+      if (err2 != hipSuccess || cus <= 0)
+        return fail(GFA_ERR_LAUNCH, "cannot read the CU count of device %d: %s", dev, hipGetErrorString(err2));
+      if (restore != hipSuccess)
+        return fail(GFA_ERR_LAUNCH, "hipSetDevice(%d) restoring the caller's device failed: %s", cur,
+                    hipGetErrorString(restore));
+      d.cus = cus;
+      base = static_cast<unsigned*>(p);
+      d.base.store(base, std::memory_order_release);
+    }
+  }
+  if (nblocks <= d.cus) return GFA_OK;  // one round: nothing to balance
+  unsigned* c = base + (size_t)(d.next.fetch_add(1, std::memory_order_relaxed) % kWqSlots) * kWqStride;
+  hipLaunchKernelGGL(wq_reset_kernel, dim3(1), dim3(64), 0, stream, c);
+  if ((err = hipGetLastError()) != hipSuccess)
+    return fail(GFA_ERR_LAUNCH, "work-queue reset launch failed: %s", hipGetErrorString(err));
+  q->wq = c;
+  q->grid = d.cus;
+  return GFA_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* gfa_last_error(void) { return g_err; }
+
+int gfa_set_runtime_scheduling(int32_t enable) {
+  if (enable < 0) return g_runtime_scheduling.load();
+  return g_runtime_scheduling.exchange(enable ? 1 : 0);
+}
 
 int gfa_version(void) { return GFA_VERSION; }
 
@@ -295,6 +387,7 @@ int gfa_fwd(const gfa_fwd_args* a) {
                 GFA_LSE_LD(a->seq_len));
   p.g = make_qgrid(p.B, p.Hkv, p.R, p.N, nw);
   if (p.g.nblocks <= 0) return fail(GFA_ERR_INVALID_ARGUMENT, "empty grid");
+  if ((rc = setup_queue(static_cast<hipStream_t>(a->stream), a->head_dim, p.g.nblocks, &p.sched))) return rc;
   const hipError_t err = gfa::launch_fwd(p, a->head_dim, bkv, nw, a->dtype == GFA_DTYPE_BF16, cap, drop,
                                          static_cast<hipStream_t>(a->stream));
   if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "forward launch failed: %s", hipGetErrorString(err));
@@ -396,6 +489,7 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves / e->dq_split);
   hipError_t err = hipSuccess;
   if (stages & GFA_BWD_DQ) {
+    if ((rc = setup_queue(stream, a->head_dim, pq.g.nblocks, &pq.sched))) return rc;
     err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, e->dq_split, bf16, cap, drop, stream);
     if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dQ launch failed: %s", hipGetErrorString(err));
   }

@@ -28,7 +28,7 @@ namespace gfa {
 constexpr bool dq_stages_rows(int D, int split) { return split == 1 && D >= 128; }
 
 template <int D, int BKV, bool IS_BF16, int NW, int SPLIT, bool CAP, bool DROP>
-__global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p) {
+__global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_arg) {
   constexpr int DH = D / SPLIT;  // head-dim slice of dQ^T one wave accumulates
   constexpr int KT = D / 16;     // k-steps of a score chain (always the full head dim)
   constexpr int DBH = DH / 32;
@@ -58,6 +58,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
   __shared__ __attribute__((aligned(1024))) char xch_raw[XCH > 0 ? (NW / 2) * XCH : 16];
+  __shared__ int work_slot[2];  // the block the run-time work hand-out gave the workgroup
   // STAGE: each wave stages its dO rows, then its O rows, and at the end its dQ rows in its
   // TILE-byte block of this launch-sized array (its Q rows go to one of the tile buffers, idle
   // before the loop). Dynamic, so the compiler's occupancy estimate (static LDS only) is that of
@@ -79,7 +80,13 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
   const int h = lane >> 5;
   const int l32 = lane & 31;
 
-  int lid = xcd_remap(blockIdx.x, p.g.nblocks, p.g.n_hg);
+  // One block of the static grid (vblock = its workgroup id there): the body below, run once per
+  // block the workgroup is given.
+  // D=512 (DYN): the host may run the kernel as a persistent grid, several blocks per workgroup.
+  constexpr bool DYN = D == 512;
+  auto body = [&](const int vblock) __attribute__((always_inline)) {
+  const BwdDqParams& p = DYN ? *kernel_args<BwdDqParams>() : p_arg;
+  int lid = xcd_remap(vblock, p.g.nblocks, p.g.n_hg);
   const int hg = lid % p.g.n_hg;
   lid /= p.g.n_hg;
   const int kvh = lid % p.Hkv;
@@ -501,6 +508,28 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p)
       }
     }
   }
+  };
+
+  // Static grid: the workgroup's own block. Run-time hand-out (p.sched.wq): blocks from the
+  // per-XCD queues until all are empty; the barrier that publishes a block also keeps every wave's
+  // LDS use of the previous block ahead of the next one's copies.
+  if constexpr (!DYN) {
+    body((int)blockIdx.x);
+    return;
+  }
+  const bool dyn = p_arg.sched.wq != nullptr;
+  WorkFetch wf;
+  if (dyn) wf.init(p_arg.sched.wq, p_arg.g.nblocks);
+  int slot = 0;
+  auto fetch = [&]() __attribute__((always_inline)) {
+    if (!dyn) return -1;
+    if (threadIdx.x == 0) work_slot[slot] = wf.next();
+    barrier_lds();
+    const int v = __builtin_amdgcn_readfirstlane(work_slot[slot]);
+    slot ^= 1;  // the next hand-out writes the other slot, so no wave reads a slot being rewritten
+    return v;
+  };
+  for (int vb = dyn ? fetch() : (int)blockIdx.x; vb >= 0; vb = fetch()) body(vb);
 }
 
 // Explicit instantiations of every built variant (device code and host launch stubs), plain and
@@ -522,13 +551,13 @@ template <int D, int BKV, bool IS_BF16, int NW, int SPLIT>
 static hipError_t launch_dq_t(const BwdDqParams& p, bool cap, bool drop, hipStream_t stream) {
   const unsigned stage_bytes = dq_stages_rows(D, SPLIT) ? NW * BKV * D * 2 : 0;  // the kernel's stage_raw
   if (cap) {
-    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, true, false>), dim3(p.g.nblocks), dim3(NW * 64),
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, true, false>), dim3(p.sched.grid), dim3(NW * 64),
                        stage_bytes, stream, p);
   } else if (drop) {
-    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, false, true>), dim3(p.g.nblocks), dim3(NW * 64),
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, false, true>), dim3(p.sched.grid), dim3(NW * 64),
                        stage_bytes, stream, p);
   } else {
-    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, false, false>), dim3(p.g.nblocks), dim3(NW * 64),
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BKV, IS_BF16, NW, SPLIT, false, false>), dim3(p.sched.grid), dim3(NW * 64),
                        stage_bytes, stream, p);
   }
   return hipGetLastError();

@@ -598,6 +598,48 @@ __device__ __forceinline__ void mma_tr_accumulate_b(f32x16 (&acc)[DB], const cha
   }
 }
 
+// The kernel's argument block (the kernels take one struct, at offset 0 of the kernarg segment),
+// through a pointer the compiler cannot see through: a kernel that runs several blocks reads its
+// arguments per block from the kernarg segment (scalar loads) instead of keeping every field live
+// in SGPRs across the block loop, which spilled them.
+template <typename P>
+__device__ __forceinline__ const P* kernel_args() {
+  const P __attribute__((address_space(4)))* a =
+      (const P __attribute__((address_space(4)))*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(a));
+  return (const P*)a;
+}
+
+// Run-time hand-out of a static grid's blocks to a persistent grid (WorkQueue in gfa_params.h).
+// One lane calls next(): it takes the next block of its XCD's queue (the blocks b with b % 8 ==
+// the XCD, in order), then, once that is empty, of the other XCDs' queues in turn; -1 when all are
+// empty. Faster XCDs thereby take more blocks, and no CU waits behind the hardware's in-order
+// dispatch. An emptied queue is never asked again by the same workgroup, so every workgroup ends
+// after at most eight failed takes.
+struct WorkFetch {
+  unsigned* ctr;
+  int nblocks;
+  int xcd;
+  int tried;  // queues found empty so far
+
+  __device__ __forceinline__ void init(unsigned* c, int n) {
+    ctr = c;
+    nblocks = n;
+    xcd = (int)(__builtin_amdgcn_s_getreg(0xF814) & 7);  // HW_REG_XCC_ID: this workgroup's XCD
+    tried = 0;
+  }
+  __device__ __forceinline__ int next() {
+    while (tried < 8) {
+      const int x = (xcd + tried) & 7;
+      const unsigned j = atomicAdd(ctr + x, 1u);
+      const long long b = 8ll * j + x;
+      if (b < nblocks) return (int)b;
+      ++tried;
+    }
+    return -1;
+  }
+};
+
 // Map the hardware workgroup id to a logical id so that GROUP consecutive logical
 // ids (which share K/V tiles) land on the same XCD. Workgroups are dispatched to
 // the 8 XCDs round-robin by blockIdx.x; the tail that does not fill 8*GROUP maps 1:1.

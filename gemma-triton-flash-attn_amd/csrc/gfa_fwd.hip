@@ -39,7 +39,7 @@
 namespace gfa {
 
 template <int D, int BKV, bool IS_BF16, int NW, int WPE, bool SEG, bool CAP, bool DROP>
-__global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
+__global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p_arg) {
   constexpr int KT = D / 16;   // MFMA k-steps over the head dim
   constexpr int DB = D / 32;   // 32-row blocks of the O^T accumulator
   constexpr int SB = BKV / 32; // 32-key score blocks per tile
@@ -62,6 +62,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
   __shared__ int redo_flag;
+  __shared__ int work_slot[2];  // the block the run-time work hand-out gave the workgroup
   char GFA_LDS* const K0 = (char GFA_LDS*)k_lds0;
   char GFA_LDS* const K1 = (char GFA_LDS*)k_lds1;
   char GFA_LDS* const V0 = (char GFA_LDS*)v_lds0;
@@ -72,8 +73,14 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
   const int h = lane >> 5;
   const int l32 = lane & 31;
 
+  // One block of the static grid (vblock = its workgroup id there): the body below, run once per
+  // block the workgroup is given.
+  // D=512 (DYN): the host may run the kernel as a persistent grid, several blocks per workgroup.
+  constexpr bool DYN = D == 512;
+  auto body = [&](const int vblock) __attribute__((always_inline)) {
+  const FwdParams& p = DYN ? *kernel_args<FwdParams>() : p_arg;
   // ---- workgroup -> (b, kv head, head group, query super-block) ----
-  int lid = xcd_remap(blockIdx.x, p.g.nblocks, p.g.n_hg);
+  int lid = xcd_remap(vblock, p.g.nblocks, p.g.n_hg);
   const int hg = lid % p.g.n_hg;
   lid /= p.g.n_hg;
   const int kvh = lid % p.Hkv;
@@ -364,6 +371,28 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p) {
     }
   }
   if (active) store_rows_lds<D>(p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh, p.ov.sn, p.N, q0, ln, sblk);
+  };
+
+  // Static grid: the workgroup's own block. Run-time hand-out (p.sched.wq): blocks from the
+  // per-XCD queues until all are empty; the barrier that publishes a block also keeps every wave's
+  // LDS use of the previous block ahead of the next one's copies.
+  if constexpr (!DYN) {
+    body((int)blockIdx.x);
+    return;
+  }
+  const bool dyn = p_arg.sched.wq != nullptr;
+  WorkFetch wf;
+  if (dyn) wf.init(p_arg.sched.wq, p_arg.g.nblocks);
+  int slot = 0;
+  auto fetch = [&]() __attribute__((always_inline)) {
+    if (!dyn) return -1;
+    if (threadIdx.x == 0) work_slot[slot] = wf.next();
+    barrier_lds();
+    const int v = __builtin_amdgcn_readfirstlane(work_slot[slot]);
+    slot ^= 1;  // the next hand-out writes the other slot, so no wave reads a slot being rewritten
+    return v;
+  };
+  for (int vb = dyn ? fetch() : (int)blockIdx.x; vb >= 0; vb = fetch()) body(vb);
 }
 
 // Explicit instantiations of every built variant (both the device code and the host
@@ -395,10 +424,10 @@ GFA_FWD_EXT(false, true)
 template <int D, int BKV, bool IS_BF16, int NW, int WPE, bool CAP, bool DROP>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   if (p.seg_lo != nullptr) {
-    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, true, CAP, DROP>), dim3(p.g.nblocks), dim3(NW * 64), 0,
+    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, true, CAP, DROP>), dim3(p.sched.grid), dim3(NW * 64), 0,
                        stream, p);
   } else {
-    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, false, CAP, DROP>), dim3(p.g.nblocks), dim3(NW * 64), 0,
+    hipLaunchKernelGGL((fwd_kernel<D, BKV, IS_BF16, NW, WPE, false, CAP, DROP>), dim3(p.sched.grid), dim3(NW * 64), 0,
                        stream, p);
   }
   return hipGetLastError();

@@ -39,6 +39,17 @@ struct QGrid {
   int nblocks;
 };
 
+// Run-time work hand-out (optional): with `wq` set, a kernel runs as a persistent grid of `grid`
+// workgroups that take the blocks of its static grid (nblocks of them, in the static grid's order)
+// from per-XCD queues: wq[x] counts the blocks taken from queue x, which holds the blocks b with
+// b % 8 == x (the XCD the hardware would have dispatched b to). A workgroup empties its own XCD's
+// queue first, then the others. The counters are zeroed before the launch. Null: the static grid
+// (one workgroup per block, dispatched by the hardware).
+struct WorkQueue {
+  unsigned* wq;
+  int grid;  // launch grid size (the static grid's block count when wq is null)
+};
+
 // Optional segment table, (B, N) int32 each, row b at seg_lo + b * N: token t attends and is
 // attended only within keys [seg_lo[t], seg_hi[t]) (intersected with the causal / window
 // rule). Null when the problem has none (one segment per sequence).
@@ -60,6 +71,7 @@ struct FwdParams {
   int store_lse;
   int lse_ld;
   QGrid g;
+  WorkQueue sched;
 };
 
 struct BwdDqParams {
@@ -82,6 +94,7 @@ struct BwdDqParams {
   Dropout drop;      // read by the DROP instances only
   int lse_ld;
   QGrid g;
+  WorkQueue sched;
 };
 
 struct BwdDkvParams {

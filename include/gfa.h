@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define GFA_VERSION 104 /* 1.0.4: optional attention dropout (1.0.3: logit soft-capping) */
+#define GFA_VERSION 105 /* 1.0.5: run-time work distribution (1.0.4: attention dropout, 1.0.3: soft-capping) */
 
 typedef enum {
   GFA_DTYPE_FP16 = 0,
@@ -183,6 +183,19 @@ size_t gfa_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, 
  * gfa_status. */
 int gfa_config(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len, int32_t head_dim,
                gfa_config_info* out);
+
+/* Run-time work distribution of the long grids (no counterpart in the reference, whose grids the
+ * Triton runtime launches as they are): with it on (the default), the forward and dQ kernels at
+ * head_dim 512, when their grid exceeds one workgroup per CU, run as a persistent grid of one
+ * workgroup per CU that
+ * takes the static grid's blocks, in their static order, from per-XCD queues at run time (a
+ * faster XCD takes more blocks, no CU idles behind the hardware's in-order dispatch). The queue
+ * counters live in a library-owned device array, one slot per launch out of 256 used
+ * round-robin, zeroed by a one-workgroup kernel on the caller's stream before the launch; the
+ * call still allocates nothing. Every block computes exactly what it computes in the static grid,
+ * so results are bit for bit the same either way. enable = 0 launches the static grids; a
+ * negative value only queries. Process-wide; returns the setting before the call. */
+int gfa_set_runtime_scheduling(int32_t enable);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* gfa_last_error(void);

@@ -42,6 +42,19 @@ def test_library_exports_every_declared_symbol():
     assert _lib.ABI_VERSION == lib.gfa_version()
 
 
+def test_runtime_scheduling_switch():
+    """gfa_set_runtime_scheduling returns the previous setting, a negative argument only queries,
+    and the binding restores it (no kernel is launched)."""
+    lib = _lib.load()
+    before = lib.gfa_set_runtime_scheduling(-1)
+    assert before in (0, 1)
+    assert _lib.set_runtime_scheduling(False) == bool(before)
+    assert lib.gfa_set_runtime_scheduling(-1) == 0
+    assert _lib.set_runtime_scheduling(True) is False
+    assert lib.gfa_set_runtime_scheduling(-1) == 1
+    _lib.set_runtime_scheduling(bool(before))
+
+
 def test_loader_refuses_a_library_of_another_abi_version(monkeypatch):
     """A libgfa.so whose GFA_VERSION differs from the layout the ctypes structs mirror would read
     another prefix of the argument structs; load() raises instead."""
