@@ -10,10 +10,10 @@
 // MI355X design: D <= 256, one wave owns 32 query rows of one head and keeps its Q and dO
 // rows in VGPRs (B operands of S^T = K Q^T and dP^T = V dO^T, lane = query). D = 512, a wave
 // pair owns them and splits the work by role: role 0 keeps the Q rows and runs S^T, role 1
-// keeps the dO rows, computes delta and runs dP^T (starting from -delta), both over the full
-// head dim; each turns half of the score block into dS (swapping the chain-result halves it
-// needs through LDS, then the packed dS halves) and accumulates its head-dim half of dQ^T. P^T and dS^T then live on the query lanes with
-// per-lane LSE, and dQ^T += K^T dS^T reads its A operand with ds_read_b64_tr_b16 from the
+// keeps the dO rows, computes delta and runs dP^T, both over the full head dim; each turns half
+// of the score block into dS (swapping the chain-result halves it needs through LDS, then the
+// packed dS halves) and accumulates its head-dim half of dQ^T. P^T and dS^T then live on the
+// query lanes with per-lane LSE, and dQ^T += K^T dS^T reads its A operand with ds_read_b64_tr_b16 from the
 // same row-major K tile that fed S^T. K and V tiles are double-buffered in LDS via buffer
 // loads that write LDS directly; the copies of the next tile are spread over the chains.
 #include "gfa_common.h"
@@ -40,7 +40,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
   constexpr bool SHARED = SPLIT == 2;
   constexpr int XSB = 2 * 2048 + 2 * 1024;
   constexpr int XCH = SHARED ? SB * XSB : 0;  // per pair
-  static_assert(BKV % 32 == 0, "BKV must be a multiple of 32");
+  static_assert(BKV == 32, "32-key tiles: one 32 x 32 score block per tile and wave");
   static_assert(SPLIT == 1 || SPLIT == 2, "one wave or a wave pair per 32 query rows");
   static_assert(D == 64 || D == 128 || D == 256 || D == 512, "head dim must be 64, 128, 256 or 512");
   // The swizzle permutes 16-chunk groups, so a head-dim half must be whole groups.
@@ -155,8 +155,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
   // One wave: Q and dO rows (full head dim); STAGE: staged through LDS by whole-row copies and
   // read back in the operand layout, the first key tile's copies issued before the O rows are
   // read for delta. Pair: role 0 the Q rows, role 1 the dO rows (loaded per lane; the D = 512
-  // pair's prologue is a small part of its blocks); role 1 also computes delta (it starts its
-  // dP^T chain from -delta, so role 0 never needs delta itself).
+  // pair's prologue is a small part of its blocks); role 1 also computes delta and hands it to
+  // role 0 below.
   // The row's LSE first: its load then overlaps the row copies.
   const float lse_log2 = p.lse[((int64_t)b * p.Hq + head) * p.lse_ld + qrow] * kLog2e;
   i16x8 qf[KT];                      // Q rows (one wave / role 0) or dO rows (role 1)
@@ -226,33 +226,19 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
     for (int kk = 0; kk < KT; ++kk) pin_vgpr(df[kk]);
   }
   const float delta = halves_sum(dpart);  // stored after the loop
-  // D >= 256: the dP^T chain starts from -delta (lane = query), so it yields dP - delta
-  // directly and dS = P (dP - delta) costs one multiply (16 AGPRs, which the one-wave-per-SIMD
-  // budget has; at D <= 128 they would cost an occupancy step, so the subtraction stays).
-  // In a pair only role 1 runs that chain.
   // The S^T and dP^T chains accumulate in VGPRs through inline-asm MFMAs (mma32_vgpr), so the dS
-  // work and the pair's exchange read them without AGPR moves (16-32 per tile); a VGPR chain
-  // cannot start from the AGPR-held -delta, so dS subtracts it (in a pair, role 1 hands delta
-  // to role 0 once).
-  constexpr bool VCHAIN = SB == 1;
-  constexpr bool DP_FROM_DELTA = D >= 256 && !DROP && !VCHAIN;  // DROP scales dP by the mask first
-  f32x16 neg_delta = f32x16{};
-  if constexpr (DP_FROM_DELTA) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) neg_delta[r] = dh == SPLIT - 1 ? -delta : 0.f;
-  }
-  // A pair that subtracts delta in dS (DROP, VCHAIN): both roles subtract it from their dP half,
-  // but only role 1 holds the dO rows it comes from; it hands delta over through the pair's
-  // exchange area (idle until the first tile step, which starts behind a barrier).
-  float delta_pair = delta;
-  if constexpr (SPLIT == 2 && !DP_FROM_DELTA) {
+  // work and the pair's exchange read them without AGPR moves (16-32 per tile), and dS subtracts
+  // delta. In a pair both roles subtract it from their dP half, but only role 1 holds the dO rows
+  // it comes from: it hands delta over through the pair's exchange area (idle until the first
+  // tile step, which starts behind a barrier). (Started from -delta in AGPRs instead, the dP^T
+  // chain yields dP - delta directly; with the chain in VGPRs the subtraction measured faster.)
+  float delta_row = delta;
+  if constexpr (SPLIT == 2) {
     float GFA_LDS* const slot = reinterpret_cast<float GFA_LDS*>(xch + (wave >> 1) * XCH) + lane;
     if (dh == 1) *slot = delta;
     barrier_lds();
-    delta_pair = *slot;
+    delta_row = *slot;
   }
-  const float delta_left = DP_FROM_DELTA ? 0.f : delta_pair;  // what dS still subtracts
-  if constexpr (DP_FROM_DELTA) pin_agpr(neg_delta);       // the chain's C operand lives there
 
   f32x16 acc[DBH];
 #pragma unroll
@@ -327,7 +313,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
         const float sv = RO == 0 ? own[sb][MH + i] : w[i >> 2][i & 3];
         const float dpv = RO == 1 ? own[sb][MH + i] : w[i >> 2][i & 3];
         const int key = k0 + sb * 32 + 8 * ((MH + i) >> 2) + 4 * h + (i & 3);
-        ds[i] = p_of(sv) * (DP_FROM_DELTA ? dpv : dp_kept(dpv, key) - delta_left);
+        ds[i] = p_of(sv) * (dp_kept(dpv, key) - delta_row);
       }
       if (need_mask) {
 #pragma unroll
@@ -363,22 +349,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
     // straight-line body keeps the accumulators resident in registers.
     f32x16 s[SB], dp[SB];
     i16x8 dsb[BKV / 16];  // dS^T, packed 16-bit: the B operand of dQ^T += K^T dS^T
-    if constexpr (VCHAIN && SPLIT == 1) {
+    if constexpr (SPLIT == 1) {
       s[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(kt, koff, qf, [&](int i) { kload.load_part(i, rn, kn); });
       __builtin_amdgcn_sched_barrier(0);
       dp[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(vt, koff, df, [&](int i) { vload.load_part(i, rn, vn); });
       __builtin_amdgcn_sched_barrier(0);
-    } else if constexpr (SPLIT == 1) {
-      s[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, NI>(kt, koff, 0, qf, [&](int i) { kload.load_part(i, rn, kn); });
-      __builtin_amdgcn_sched_barrier(0);
-      dp[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, NI>(vt, koff, 0, df, [&](int i) { vload.load_part(i, rn, vn); },
-                                                    neg_delta);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int sb = 1; sb < SB; ++sb) {
-        s[sb] = mma_chain1_lds<IS_BF16, KT, 4>(kt, koff, sb * 32 * (2 * D), qf);
-        dp[sb] = mma_chain1_lds<IS_BF16, KT, 4>(vt, koff, sb * 32 * (2 * D), df) + neg_delta;
-      }
     } else {
       // This role's chain over the full head dim, with both tiles' copies spread over it;
       // then the swap: each wave reads S^T and dP^T - delta from the exchange slots.
@@ -387,7 +362,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
       // reads from the in-flight copies (with a select it waits for the copies every product:
       // 2.5x slower).
       f32x16 own[SB];
-      auto run = [&](const char GFA_LDS* ct, const f32x16& init) __attribute__((always_inline)) {
+      auto run = [&](const char GFA_LDS* ct) __attribute__((always_inline)) {
         auto ld = [&](int i) {
           if (i < NI) {
             kload.load_part(i, rn, kn);
@@ -395,19 +370,13 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
             vload.load_part(i - NI, rn, vn);
           }
         };
-        if constexpr (VCHAIN) {
-          own[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, 2 * NI>(ct, koff, qf, ld);
-        } else {
-          own[0] = mma_chain1_lds_ld<IS_BF16, KT, 4, 2 * NI>(ct, koff, 0, qf, ld, init);
-        }
+        own[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, 2 * NI>(ct, koff, qf, ld);
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int sb = 1; sb < SB; ++sb) own[sb] = mma_chain1_lds<IS_BF16, KT, 4>(ct, koff, sb * 32 * (2 * D), qf) + init;
       };
       if (dh == 0) {
-        run(kt, f32x16{});
+        run(kt);
       } else {
-        run(vt, neg_delta);
+        run(vt);
       }
       if (dh == 0) {
         shared_ds(std::integral_constant<int, 0>{}, own, dsb, k0);
@@ -422,8 +391,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float dpd = DP_FROM_DELTA ? dp[sb][r]
-                                        : dp_kept(dp[sb][r], k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) - delta_left;
+        const float dpd = dp_kept(dp[sb][r], k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) - delta_row;
         s[sb][r] = p_of(s[sb][r]) * dpd;
       }
     }
