@@ -58,7 +58,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
   __shared__ __attribute__((aligned(1024))) char xch_raw[XCH > 0 ? (NW / 2) * XCH : 16];
-  __shared__ int work_slot[2];  // the block the run-time work hand-out gave the workgroup
+  __shared__ int work_slot[3];  // the block the run-time work hand-out gave the workgroup (two slots), its state
   // STAGE: each wave stages its dO rows, then its O rows, and at the end its dQ rows in its
   // TILE-byte block of this launch-sized array (its Q rows go to one of the tile buffers, idle
   // before the loop). Dynamic, so the compiler's occupancy estimate (static LDS only) is that of
@@ -485,19 +485,18 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
     body((int)blockIdx.x);
     return;
   }
-  const bool dyn = p_arg.sched.wq != nullptr;
-  WorkFetch wf;
-  if (dyn) wf.init(p_arg.sched.wq, p_arg.g.nblocks);
+  if (threadIdx.x == 0) work_slot[2] = 0;  // queues found empty (work_next)
   int slot = 0;
   auto fetch = [&]() __attribute__((always_inline)) {
-    if (!dyn) return -1;
-    if (threadIdx.x == 0) work_slot[slot] = wf.next();
+    const BwdDqParams& pa = *kernel_args<BwdDqParams>();
+    if (pa.sched.wq == nullptr) return -1;
+    if (threadIdx.x == 0) work_slot[slot] = work_next(pa.sched.wq, pa.g.nblocks, &work_slot[2]);
     barrier_lds();
     const int v = __builtin_amdgcn_readfirstlane(work_slot[slot]);
     slot ^= 1;  // the next hand-out writes the other slot, so no wave reads a slot being rewritten
     return v;
   };
-  for (int vb = dyn ? fetch() : (int)blockIdx.x; vb >= 0; vb = fetch()) body(vb);
+  for (int vb = p_arg.sched.wq ? fetch() : (int)blockIdx.x; vb >= 0; vb = fetch()) body(vb);
 }
 
 // Explicit instantiations of every built variant (device code and host launch stubs), plain and

@@ -610,35 +610,31 @@ __device__ __forceinline__ const P* kernel_args() {
   return (const P*)a;
 }
 
-// Run-time hand-out of a static grid's blocks to a persistent grid (WorkQueue in gfa_params.h).
-// One lane calls next(): it takes the next block of its XCD's queue (the blocks b with b % 8 ==
-// the XCD, in order), then, once that is empty, of the other XCDs' queues in turn; -1 when all are
-// empty. Faster XCDs thereby take more blocks, and no CU waits behind the hardware's in-order
-// dispatch. An emptied queue is never asked again by the same workgroup, so every workgroup ends
-// after at most eight failed takes.
-struct WorkFetch {
-  unsigned* ctr;
-  int nblocks;
-  int xcd;
-  int tried;  // queues found empty so far
-
-  __device__ __forceinline__ void init(unsigned* c, int n) {
-    ctr = c;
-    nblocks = n;
-    xcd = (int)(__builtin_amdgcn_s_getreg(0xF814) & 7);  // HW_REG_XCC_ID: this workgroup's XCD
-    tried = 0;
-  }
-  __device__ __forceinline__ int next() {
-    while (tried < 8) {
-      const int x = (xcd + tried) & 7;
-      const unsigned j = atomicAdd(ctr + x, 1u);
-      const long long b = 8ll * j + x;
-      if (b < nblocks) return (int)b;
-      ++tried;
+// Run-time hand-out of a static grid's blocks to a persistent grid (WorkQueue in gfa_params.h),
+// called by one lane of the workgroup: takes the next block of its XCD's queue (the blocks b with
+// b % 8 == the XCD, in order), then, once that is empty, of the other XCDs' queues in turn; -1
+// when all are empty. Faster XCDs thereby take more blocks, and no CU waits behind the hardware's
+// in-order dispatch. `tried` (the workgroup's count of queues found empty, zero before its first
+// call) lives in LDS, so no register holds the hand-out's state across a block; an emptied queue
+// is never asked again by the same workgroup, so every workgroup ends after at most eight failed
+// takes.
+__device__ __forceinline__ int work_next(unsigned* ctr, int nblocks, int* tried) {
+  const int xcd = (int)(__builtin_amdgcn_s_getreg(0xF814) & 7);  // HW_REG_XCC_ID: this workgroup's XCD
+  int t = *tried;
+  int b = -1;
+  while (t < 8) {
+    const int x = (xcd + t) & 7;
+    const unsigned j = atomicAdd(ctr + x, 1u);
+    const long long cand = 8ll * j + x;
+    if (cand < nblocks) {
+      b = (int)cand;
+      break;
     }
-    return -1;
+    ++t;
   }
-};
+  *tried = t;
+  return b;
+}
 
 // Map the hardware workgroup id to a logical id so that GROUP consecutive logical
 // ids (which share K/V tiles) land on the same XCD. Workgroups are dispatched to

@@ -62,7 +62,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p_arg
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
   __shared__ int redo_flag;
-  __shared__ int work_slot[2];  // the block the run-time work hand-out gave the workgroup
+  __shared__ int work_slot[3];  // the block the run-time work hand-out gave the workgroup (two slots), its state
   char GFA_LDS* const K0 = (char GFA_LDS*)k_lds0;
   char GFA_LDS* const K1 = (char GFA_LDS*)k_lds1;
   char GFA_LDS* const V0 = (char GFA_LDS*)v_lds0;
@@ -380,19 +380,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p_arg
     body((int)blockIdx.x);
     return;
   }
-  const bool dyn = p_arg.sched.wq != nullptr;
-  WorkFetch wf;
-  if (dyn) wf.init(p_arg.sched.wq, p_arg.g.nblocks);
+  if (threadIdx.x == 0) work_slot[2] = 0;  // queues found empty (work_next)
   int slot = 0;
   auto fetch = [&]() __attribute__((always_inline)) {
-    if (!dyn) return -1;
-    if (threadIdx.x == 0) work_slot[slot] = wf.next();
+    const FwdParams& pa = *kernel_args<FwdParams>();
+    if (pa.sched.wq == nullptr) return -1;
+    if (threadIdx.x == 0) work_slot[slot] = work_next(pa.sched.wq, pa.g.nblocks, &work_slot[2]);
     barrier_lds();
     const int v = __builtin_amdgcn_readfirstlane(work_slot[slot]);
     slot ^= 1;  // the next hand-out writes the other slot, so no wave reads a slot being rewritten
     return v;
   };
-  for (int vb = dyn ? fetch() : (int)blockIdx.x; vb >= 0; vb = fetch()) body(vb);
+  for (int vb = p_arg.sched.wq ? fetch() : (int)blockIdx.x; vb >= 0; vb = fetch()) body(vb);
 }
 
 // Explicit instantiations of every built variant (both the device code and the host
