@@ -183,13 +183,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void fwd_kernel(const FwdParams p_arg
   // One key tile: wait for it, then S^T = K Q^T with the copy of tile t+1 into the other
   // buffers spread over the chain, softmax against the fixed reference max, O^T += V^T P^T.
   constexpr int NI = TileLoader<D, BKV, NW>::NI;  // copy instructions per tile and wave
-  // bf16 at D <= 256 (LAZY): the tile's row max is taken only while some row of the wave has no
-  // reference max yet (a wave-uniform test), and overflow is judged once per pass from the row
-  // sum: a P above 2^kMargin makes l above it too. The rare redo then first finds the exact row
-  // max in a pass that runs the S^T chains alone (MODE 1). 6% faster at D=64, 3% at D=128, 1% at
-  // D=256; at D=512 (one wave per SIMD, the max hidden under the chain) 1% slower. fp16's margin
-  // (2^15) is within reach of a long row's sum, so fp16 keeps the per-tile max and check.
-  constexpr bool LAZY = IS_BF16 && D <= 256;
+  // bf16 (LAZY): the tile's row max is taken only while some row of the wave has no reference
+  // max yet (a wave-uniform test), and overflow is judged once per pass from the row sum: a P
+  // above 2^kMargin makes l above it too. The rare redo then first finds the exact row max in a
+  // pass that runs the S^T chains alone (MODE 1). 6% faster at D=64, 3% at D=128, 1% at D=256 and
+  // D=512 (at D=512 1% slower while the score chain ran in AGPRs). fp16's margin (2^15) is within
+  // reach of a long row's sum, so fp16 keeps the per-tile max and check.
+  constexpr bool LAZY = IS_BF16;
   // One wave per SIMD with O^T pinned in AGPRs: the S^T chain accumulates in VGPRs through
   // inline-asm MFMAs (mma32_vgpr); built from the builtin it runs in AGPRs, and the softmax then
   // reads its scores back with AGPR moves.
