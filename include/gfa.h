@@ -185,16 +185,19 @@ int gfa_config(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len
                gfa_config_info* out);
 
 /* Run-time work distribution of the long grids (no counterpart in the reference, whose grids the
- * Triton runtime launches as they are): with it on (the default), the forward and dQ kernels at
+ * Triton runtime launches as they are). With it on (the default), the forward and dQ kernels at
  * head_dim 512, when their grid exceeds one workgroup per CU, run as a persistent grid of one
- * workgroup per CU that
- * takes the static grid's blocks, in their static order, from per-XCD queues at run time (a
- * faster XCD takes more blocks, no CU idles behind the hardware's in-order dispatch). The queue
- * counters live in a library-owned device array, one slot per launch out of 256 used
- * round-robin, zeroed by a one-workgroup kernel on the caller's stream before the launch; the
- * call still allocates nothing. Every block computes exactly what it computes in the static grid,
- * so results are bit for bit the same either way. enable = 0 launches the static grids; a
- * negative value only queries. Process-wide; returns the setting before the call. */
+ * workgroup per CU that takes the static grid's blocks, in their static order, from per-XCD
+ * queues at run time (a faster XCD takes more blocks, no CU idles behind the hardware's in-order
+ * dispatch). The queue counters live in a library-owned device array, one slot per launch out of
+ * 256 used round-robin, zeroed by a one-workgroup kernel on the caller's stream before the
+ * launch; the call still allocates nothing. Launches that overlap in time on different streams
+ * must not share a slot: they must be fewer than 256 persistent launches apart. A launch captured
+ * into a HIP graph keeps its slot for every replay, so graphs whose replays overlap on different
+ * streams must not have been captured a multiple of 256 persistent launches apart (or must run
+ * with this switched off). Every block computes exactly what it computes in the static grid, so
+ * results are bit for bit the same either way. enable = 0 launches the static grids; a negative
+ * value only queries. Process-wide; returns the setting before the call. */
 int gfa_set_runtime_scheduling(int32_t enable);
 
 /* Message of the last failing call on this thread ("" if none). */
