@@ -227,13 +227,20 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
   }
   const float delta = halves_sum(dpart);  // stored after the loop
   // The S^T and dP^T chains accumulate in VGPRs through inline-asm MFMAs (mma32_vgpr), so the dS
-  // work and the pair's exchange read them without AGPR moves (16-32 per tile), and dS subtracts
-  // delta. In a pair both roles subtract it from their dP half, but only role 1 holds the dO rows
-  // it comes from: it hands delta over through the pair's exchange area (idle until the first
-  // tile step, which starts behind a barrier). (Started from -delta in AGPRs instead, the dP^T
-  // chain yields dP - delta directly; with the chain in VGPRs the subtraction measured faster.)
+  // work and the pair's exchange read them without AGPR moves (16-32 per tile). The dP^T chain
+  // starts from -delta (the lane's query; a block of 16 VGPRs the chain reads as its C operand),
+  // so it yields dP - delta and dS costs one multiply per element; in a pair role 1 runs that
+  // chain and role 0 receives its half already shifted. DROP scales dP by the mask before delta
+  // is subtracted, so there the chain starts from zero and dS subtracts delta: in a pair both
+  // roles then subtract it from their dP half, but only role 1 holds the dO rows it comes from,
+  // and it hands delta over through the pair's exchange area (idle until the first tile step,
+  // which starts behind a barrier).
+  constexpr bool DP_FROM_DELTA = !DROP;
+  f32x16 neg_delta;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) neg_delta[r] = -delta;
   float delta_row = delta;
-  if constexpr (SPLIT == 2) {
+  if constexpr (SPLIT == 2 && !DP_FROM_DELTA) {
     float GFA_LDS* const slot = reinterpret_cast<float GFA_LDS*>(xch + (wave >> 1) * XCH) + lane;
     if (dh == 1) *slot = delta;
     barrier_lds();
@@ -313,7 +320,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
         const float sv = RO == 0 ? own[sb][MH + i] : w[i >> 2][i & 3];
         const float dpv = RO == 1 ? own[sb][MH + i] : w[i >> 2][i & 3];
         const int key = k0 + sb * 32 + 8 * ((MH + i) >> 2) + 4 * h + (i & 3);
-        ds[i] = p_of(sv) * (dp_kept(dpv, key) - delta_row);
+        ds[i] = p_of(sv) * (DP_FROM_DELTA ? dpv : dp_kept(dpv, key) - delta_row);
       }
       if (need_mask) {
 #pragma unroll
@@ -352,7 +359,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
     if constexpr (SPLIT == 1) {
       s[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(kt, koff, qf, [&](int i) { kload.load_part(i, rn, kn); });
       __builtin_amdgcn_sched_barrier(0);
-      dp[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(vt, koff, df, [&](int i) { vload.load_part(i, rn, vn); });
+      dp[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(vt, koff, df, [&](int i) { vload.load_part(i, rn, vn); },
+                                                         DP_FROM_DELTA ? &neg_delta : nullptr);
       __builtin_amdgcn_sched_barrier(0);
     } else {
       // This role's chain over the full head dim, with both tiles' copies spread over it;
@@ -362,7 +370,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
       // reads from the in-flight copies (with a select it waits for the copies every product:
       // 2.5x slower).
       f32x16 own[SB];
-      auto run = [&](const char GFA_LDS* ct) __attribute__((always_inline)) {
+      auto run = [&](const char GFA_LDS* ct, const f32x16* c0) __attribute__((always_inline)) {
         auto ld = [&](int i) {
           if (i < NI) {
             kload.load_part(i, rn, kn);
@@ -370,13 +378,13 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
             vload.load_part(i - NI, rn, vn);
           }
         };
-        own[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, 2 * NI>(ct, koff, qf, ld);
+        own[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, 2 * NI>(ct, koff, qf, ld, c0);
         __builtin_amdgcn_sched_barrier(0);
       };
       if (dh == 0) {
-        run(kt);
+        run(kt, nullptr);
       } else {
-        run(vt);
+        run(vt, DP_FROM_DELTA ? &neg_delta : nullptr);
       }
       if (dh == 0) {
         shared_ds(std::integral_constant<int, 0>{}, own, dsb, k0);
@@ -391,7 +399,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
     for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float dpd = dp_kept(dp[sb][r], k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) - delta_row;
+        const float dpd = DP_FROM_DELTA ? dp[sb][r]
+                                        : dp_kept(dp[sb][r], k0 + sb * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) - delta_row;
         s[sb][r] = p_of(s[sb][r]) * dpd;
       }
     }

@@ -429,15 +429,28 @@ __device__ __forceinline__ void mma32_vgpr(f32x16& c, const i16x8& a, const i16x
     }
   }
 }
+// First product of a VGPR chain started from c0 (C = c0, a VGPR block the chain does not write).
+// The leading s_nop covers the two wait states a VALU write of c0 needs before an MFMA reads it
+// as its C operand, in case the compiler materializes c0 right before the chain.
+template <bool IS_BF16>
+__device__ __forceinline__ void mma32_vgpr_from(f32x16& d, const i16x8& a, const i16x8& b, const f32x16& c0) {
+  if constexpr (IS_BF16) {
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(a), "v"(b), "v"(c0));
+  } else {
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %3" : "=&v"(d) : "v"(a), "v"(b), "v"(c0));
+  }
+}
 // The compiler cannot see the pass count of an MFMA written in inline assembly, so it inserts no
 // wait states before the first read of its result. An 8-pass XDL op on gfx950 needs 12 before a
 // VALU, LDS or memory instruction reads its VGPR result; 16 are inserted here.
 __device__ __forceinline__ void mfma_result_fence(f32x16& c) { asm volatile("s_nop 7\n\ts_nop 7" : "+v"(c)); }
 
-// mma_chain1_lds_ld with the chain accumulating in VGPRs (mma32_vgpr), started from zero.
+// mma_chain1_lds_ld with the chain accumulating in VGPRs (mma32_vgpr), started from zero or, with
+// c0, from that VGPR block (mma32_vgpr_from).
 template <bool IS_BF16, int KT, int PF, int NL, typename LD>
 __device__ __forceinline__ f32x16 mma_chain1_lds_ld_vgpr(const char GFA_LDS* tile, const int (&koff)[8],
-                                                         const i16x8 (&bf)[KT], LD&& ld) {
+                                                         const i16x8 (&bf)[KT], LD&& ld,
+                                                         const f32x16* c0 = nullptr) {
   static_assert(PF <= KT && NL >= 1 && KT % NL == 0, "bad chain shape");
   constexpr int EV = KT / NL;
   f32x16 c;
@@ -448,7 +461,9 @@ __device__ __forceinline__ f32x16 mma_chain1_lds_ld_vgpr(const char GFA_LDS* til
   for (int kk = 0; kk < KT; ++kk) {
     const i16x8 cur = a[kk % PF];
     if (kk + PF < KT) a[kk % PF] = lds_read16(tile, koff[(kk + PF) & 7] + 256 * ((kk + PF) >> 3));
-    if (kk == 0) {
+    if (kk == 0 && c0 != nullptr) {
+      mma32_vgpr_from<IS_BF16>(c, cur, bf[kk], *c0);
+    } else if (kk == 0) {
       mma32_vgpr<IS_BF16, true>(c, cur, bf[kk]);
     } else {
       mma32_vgpr<IS_BF16, false>(c, cur, bf[kk]);
