@@ -356,7 +356,18 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(const BwdDqParams p_
     // straight-line body keeps the accumulators resident in registers.
     f32x16 s[SB], dp[SB];
     i16x8 dsb[BKV / 16];  // dS^T, packed 16-bit: the B operand of dQ^T += K^T dS^T
-    if constexpr (SPLIT == 1) {
+    if constexpr (SPLIT == 1 && D <= 128) {
+      // D <= 128: the two chains interleaved product by product (two fragments ahead each), so
+      // no MFMA waits on the one before it: 1.2% (D=128) and 1.5% (D=64) faster; at D=256 1% slower.
+      mma_chain2_lds_ld_vgpr<IS_BF16, KT, 2, 2 * NI>(s[0], dp[0], kt, vt, koff, qf, df, [&](int i) {
+        if (i < NI) {
+          kload.load_part(i, rn, kn);
+        } else {
+          vload.load_part(i - NI, rn, vn);
+        }
+      }, DP_FROM_DELTA ? &neg_delta : nullptr);
+      __builtin_amdgcn_sched_barrier(0);
+    } else if constexpr (SPLIT == 1) {
       s[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(kt, koff, qf, [&](int i) { kload.load_part(i, rn, kn); });
       __builtin_amdgcn_sched_barrier(0);
       dp[0] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(vt, koff, df, [&](int i) { vload.load_part(i, rn, vn); },

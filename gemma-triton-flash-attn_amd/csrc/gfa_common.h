@@ -474,6 +474,51 @@ __device__ __forceinline__ f32x16 mma_chain1_lds_ld_vgpr(const char GFA_LDS* til
   return c;
 }
 
+// Two independent VGPR chains interleaved product by product: cA over the rows of tile tA with
+// fragments bfA (from zero), cB over tile tB with bfB (from zero, or from c0B). Back-to-back
+// MFMAs then never depend on each other (a dependent chain on one accumulator issues a product
+// every ~38-40 cycles instead of 32). NL copy instructions (ld(i)) are spread over the 2 KT
+// products.
+template <bool IS_BF16, int KT, int PF, int NL, typename LD>
+__device__ __forceinline__ void mma_chain2_lds_ld_vgpr(f32x16& cA, f32x16& cB, const char GFA_LDS* tA,
+                                                       const char GFA_LDS* tB, const int (&koff)[8],
+                                                       const i16x8 (&bfA)[KT], const i16x8 (&bfB)[KT], LD&& ld,
+                                                       const f32x16* c0B = nullptr) {
+  static_assert(PF <= KT && NL >= 1 && (2 * KT) % NL == 0, "bad chain shape");
+  constexpr int EV = 2 * KT / NL;
+  i16x8 aA[PF], aB[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    aA[i] = lds_read16(tA, koff[i & 7] + 256 * (i >> 3));
+    aB[i] = lds_read16(tB, koff[i & 7] + 256 * (i >> 3));
+  }
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const i16x8 curA = aA[kk % PF];
+    const i16x8 curB = aB[kk % PF];
+    if (kk + PF < KT) {
+      aA[kk % PF] = lds_read16(tA, koff[(kk + PF) & 7] + 256 * ((kk + PF) >> 3));
+      aB[kk % PF] = lds_read16(tB, koff[(kk + PF) & 7] + 256 * ((kk + PF) >> 3));
+    }
+    if (kk == 0) {
+      mma32_vgpr<IS_BF16, true>(cA, curA, bfA[kk]);
+    } else {
+      mma32_vgpr<IS_BF16, false>(cA, curA, bfA[kk]);
+    }
+    if ((2 * kk) % EV == 0) ld((2 * kk) / EV);
+    if (kk == 0 && c0B != nullptr) {
+      mma32_vgpr_from<IS_BF16>(cB, curB, bfB[kk], *c0B);
+    } else if (kk == 0) {
+      mma32_vgpr<IS_BF16, true>(cB, curB, bfB[kk]);
+    } else {
+      mma32_vgpr<IS_BF16, false>(cB, curB, bfB[kk]);
+    }
+    if ((2 * kk + 1) % EV == 0) ld((2 * kk + 1) / EV);
+  }
+  mfma_result_fence(cA);
+  mfma_result_fence(cB);
+}
+
 // mma_chain1_lds_ld_b with the chain accumulating in VGPRs (mma32_vgpr), started from zero.
 template <bool IS_BF16, int KT, int PF, int NL, typename LD>
 __device__ __forceinline__ f32x16 mma_chain1_lds_ld_b_vgpr(const char GFA_LDS* tile, int koff0, const i16x8 (&bf)[KT],
