@@ -41,6 +41,10 @@ PAIRS = {
     "d256_swa": [(2, 16, 8, 2048, 256, True, 256, torch.bfloat16, 0), (1, 4, 2, 130, 256, True, 64, torch.float16, 0)],
     "split_partials": [(1, 8, 1, 2048, 512, True, 0, torch.bfloat16, 4), (1, 4, 2, 200, 128, False, 0, torch.float16, 2)],
     "d64_split8": [(2, 8, 8, 777, 64, True, 100, torch.bfloat16, 8), (1, 2, 1, 65, 64, True, 0, torch.bfloat16, 2)],
+    # the first call's dQ grid (1,024 blocks) runs persistent, taking its blocks from the
+    # work-queue counters at run time; the second's (128) is a static grid
+    "d512_persistent_dq": [(1, 16, 2, 4096, 512, True, 0, torch.bfloat16, 1),
+                           (1, 8, 2, 1000, 512, True, 0, torch.bfloat16, 1)],
 }
 
 
