@@ -211,6 +211,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // One wave per 32 keys at D >= 256 (both accumulators fill the AGPRs): the two score chains
   // accumulate in VGPRs (mma32_vgpr), so no accumulator block is moved out and back around them.
   constexpr bool VCHAIN1 = ROLES == 1 && SB == 1 && D >= 256 && !ONE_BASE;
+  static_assert(!VCHAIN1 || KT == 16, "the dP chain computes one exponential of the S block per product");
   // Role pairs at two waves per SIMD and D=256 (register-bound): the score chains start from
   // the row statistic instead of zero, so neither LSE nor delta stays live past the chain:
   // role 0 from -LSE / scale (P = exp2(scale * log2e * acc)), role 1 from -delta (dS = P acc).
@@ -313,12 +314,19 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   }
 
   // P on the key lanes (rows = queries per register): exp2 against the row LSE, masked.
-  auto make_p = [&](f32x16 (&sc)[SB], const f32x4 (&lse)[SB][4], int q0) __attribute__((always_inline)) {
+  // exps_done: sc already holds the exponentials (computed under the dP chain), only the mask is left.
+  auto p_elem = [&](float sv, float lse) __attribute__((always_inline)) {
+    return fast_exp2(sv * p.scale_log2 - lse * kLog2e);
+  };
+  auto make_p = [&](f32x16 (&sc)[SB], const f32x4 (&lse)[SB][4], int q0, bool exps_done = false)
+                    __attribute__((always_inline)) {
     const bool need_mask = !(active && pair_full && q0 >= all_lo && q0 + BQ <= all_hi && q0 + BQ <= p.N);
+    if (!exps_done) {
 #pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
+      for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[sb][r] = fast_exp2(sc[sb][r] * p.scale_log2 - lse[sb][r >> 2][r & 3] * kLog2e);
+        for (int r = 0; r < 16; ++r) sc[sb][r] = p_elem(sc[sb][r], lse[sb][r >> 2][r & 3]);
+      }
     }
     if (need_mask) {
 #pragma unroll
@@ -631,7 +639,19 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
         if (sb == 0) {
           auto ldd = [&](int i) { dload.load_part(i, row_n, dn); };
           if constexpr (VCHAIN1) {
-            dp[sb] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(dt, roff, sf[1], ldd);
+            if constexpr (!CAP) {
+              // P of the finished S block, one element per product of the dP chain (the
+              // exponentials issue under the matrix unit): full-causal D=256 0.2%, non-causal 0.8%.
+              dp[sb] = mma_chain1_lds_ld_vgpr_side<IS_BF16, KT, 4, NI>(dt, roff, sf[1], ldd, nullptr, [&](int kk) {
+                float x = s[0][kk];
+                asm volatile("" : "+v"(x));
+                x = p_elem(x, st[0][0][kk >> 2][kk & 3]);
+                asm volatile("" : "+v"(x));
+                s[0][kk] = x;
+              });
+            } else {
+              dp[sb] = mma_chain1_lds_ld_vgpr<IS_BF16, KT, 4, NI>(dt, roff, sf[1], ldd);
+            }
           } else {
             dp[sb] = chain_ld(std::integral_constant<int, NI>{}, dt, sf[1], ldd);
           }
@@ -643,7 +663,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
       if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
       if constexpr (DROP) {
         // dS = P (kept dP / (1 - p) - delta); dV takes the kept P / (1 - p).
-        make_p(s, st[0], q0);
+        make_p(s, st[0], q0, VCHAIN1);
 #pragma unroll
         for (int sb = 0; sb < SB; ++sb) {
 #pragma unroll
@@ -669,7 +689,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
           }
         }
       } else {
-        make_p(s, st[0], q0);
+        make_p(s, st[0], q0, VCHAIN1);
 #pragma unroll
         for (int sb = 0; sb < SB; ++sb) {
           f32x4 pv4[4];

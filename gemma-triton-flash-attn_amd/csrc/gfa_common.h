@@ -447,10 +447,14 @@ __device__ __forceinline__ void mfma_result_fence(f32x16& c) { asm volatile("s_n
 
 // mma_chain1_lds_ld with the chain accumulating in VGPRs (mma32_vgpr), started from zero or, with
 // c0, from that VGPR block (mma32_vgpr_from).
-template <bool IS_BF16, int KT, int PF, int NL, typename LD>
-__device__ __forceinline__ f32x16 mma_chain1_lds_ld_vgpr(const char GFA_LDS* tile, const int (&koff)[8],
-                                                         const i16x8 (&bf)[KT], LD&& ld,
-                                                         const f32x16* c0 = nullptr) {
+// side(kk) runs after product kk: vector work on registers the chain does not touch issues
+// between the dependent products, which leave the vector unit idle (one product every ~38
+// cycles, 32 of them matrix work). side fences its values with empty asm statements (the
+// products are volatile asm, which the scheduler keeps in order) so that they stay there.
+template <bool IS_BF16, int KT, int PF, int NL, typename LD, typename SIDE>
+__device__ __forceinline__ f32x16 mma_chain1_lds_ld_vgpr_side(const char GFA_LDS* tile, const int (&koff)[8],
+                                                              const i16x8 (&bf)[KT], LD&& ld, const f32x16* c0,
+                                                              SIDE&& side) {
   static_assert(PF <= KT && NL >= 1 && KT % NL == 0, "bad chain shape");
   constexpr int EV = KT / NL;
   f32x16 c;
@@ -469,9 +473,17 @@ __device__ __forceinline__ f32x16 mma_chain1_lds_ld_vgpr(const char GFA_LDS* til
       mma32_vgpr<IS_BF16, false>(c, cur, bf[kk]);
     }
     if (kk % EV == 0) ld(kk / EV);
+    side(kk);
   }
   mfma_result_fence(c);
   return c;
+}
+
+template <bool IS_BF16, int KT, int PF, int NL, typename LD>
+__device__ __forceinline__ f32x16 mma_chain1_lds_ld_vgpr(const char GFA_LDS* tile, const int (&koff)[8],
+                                                         const i16x8 (&bf)[KT], LD&& ld,
+                                                         const f32x16* c0 = nullptr) {
+  return mma_chain1_lds_ld_vgpr_side<IS_BF16, KT, PF, NL>(tile, koff, bf, ld, c0, [](int) {});
 }
 
 // Two independent VGPR chains interleaved product by product: cA over the rows of tile tA with
