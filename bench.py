@@ -75,18 +75,25 @@ def charged_flops(w, passes):
     return (4 if passes == "fwd" else 14) * B * Hq * N * N * D
 
 
-def kernel_flops(w):
+def kernel_flops(w, materialised=False):
     """Algorithmic flops per launch of each kernel: 2*D per pair-product per attended
-    (query, key) pair; forward 2 products, dQ 3 (S, dP, dQ), dKV 4 (S, dP, dV, dK)."""
+    (query, key) pair; forward 2 products, dKV 4 (S, dP, dV, dK), dQ 3 (S, dP, dQ) in the
+    recomputing backward and 1 (dS K) in the materialised one, which reads dS from its store."""
     unit = charged_flops(w, "fwd") / 2.0  # = 2*D*pairs (causal convention)
-    return {"fwd": 2 * unit, "dq": 3 * unit, "dkv": 4 * unit}
+    return {"fwd": 2 * unit, "dq": (1 if materialised else 3) * unit, "dkv": 4 * unit}
 
 
-def kernel_bytes(w):
+def kernel_bytes(w, ds_bytes=0):
     """Algorithmic HBM bytes per launch of each kernel: every tensor the kernel must touch,
-    read or written once (16-bit Q/K/V/O/dO/dQ/dK/dV, fp32 LSE and delta)."""
+    read or written once (16-bit Q/K/V/O/dO/dQ/dK/dV, fp32 LSE and delta). ``ds_bytes`` > 0:
+    the materialised backward, whose "dkv" stage is the delta kernel (O, dO in; delta out) and
+    dK/dV writing the dS store, and whose "dq" stage reads the store and K and writes dQ."""
     B, Hq, Hkv, N, D = w["B"], w["Hq"], w["Hkv"], w["N"], w["D"]
     qsz, kvsz, rows = 2 * B * Hq * N * D, 2 * B * Hkv * N * D, 4 * B * Hq * N
+    if ds_bytes:
+        return {"fwd": 2 * qsz + 2 * kvsz + rows,
+                "dq": kvsz + ds_bytes + qsz,
+                "dkv": (2 * qsz + rows) + (2 * qsz + 4 * kvsz + 2 * rows + ds_bytes)}
     return {"fwd": 2 * qsz + 2 * kvsz + rows,             # Q, K, V in; O, LSE out
             "dq": 4 * qsz + 2 * kvsz + 2 * rows,          # Q, O, dO, K, V, LSE in; dQ, delta out
             "dkv": 2 * qsz + 4 * kvsz + 2 * rows}         # Q, dO, K, V, LSE, delta in; dK, dV out
@@ -147,7 +154,7 @@ def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd", 
 
     import gemma_triton_flash_attn_amd as gfa
     from gemma_triton_flash_attn_amd import _lib
-    from gemma_triton_flash_attn_amd.attention import _backward, _forward
+    from gemma_triton_flash_attn_amd.attention import _backward, _forward, backward_workspace
 
     print(f"[bench] {name}: {w}", file=sys.stderr, flush=True)
     q, k, v, do = make_inputs(w, device, layout)
@@ -163,6 +170,13 @@ def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd", 
         o.backward(do)
 
     res = {}
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[w["dtype"]]
+    ws_bytes, materialised = backward_workspace(w["B"], w["Hq"], w["Hkv"], w["N"], w["D"], w["causal"], w["window"], dt)
+    res["bwd_form"] = "materialised" if materialised else "recomputing"
+    res["bwd_workspace_bytes"] = ws_bytes
+    if materialised:  # the workspace beyond the (256-byte aligned) Q-split partials is the dS store
+        base = _lib.bwd_workspace_size(w["B"], w["Hq"], w["Hkv"], w["N"], w["D"], w["causal"], w["window"])
+        res["ds_store_bytes"] = ws_bytes - ((base + 255) // 256 * 256)
     ext = {} if exact else {"min_warm_ms": 100.0, "min_time_ms": 200.0}
     kext = {"min_warm_ms": 100.0, "min_time_ms": 200.0}
     with torch.no_grad():
@@ -180,7 +194,11 @@ def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd", 
         o, lse = _forward(q, k, v, w["causal"], w["window"], scale, store_lse=True)
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         delta = torch.empty(lse.shape, dtype=torch.float32, device=device)
-        bufs = (dq, dk, dv, delta)
+        # The workspace persists over the stage loops: in the materialised form the GFA_BWD_DQ
+        # stage reads the dS store the full backward below (and each GFA_BWD_DKV stage) leaves.
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+        bufs = (dq, dk, dv, delta) + ((ws,) if ws is not None else ())
+        _backward(q, k, v, o, lse, do, w["causal"], w["window"], scale, out=bufs)
         per = {
             "fwd": time_loop(lambda: _forward(q, k, v, w["causal"], w["window"], scale, store_lse=True), steps, 1,
                              **kext),
@@ -189,7 +207,7 @@ def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd", 
             "dkv": time_loop(lambda: _backward(q, k, v, o, lse, do, w["causal"], w["window"], scale,
                                                stages=_lib.GFA_BWD_DKV, out=bufs), steps, 1, **kext),
         }
-        kf = kernel_flops(w)
+        kf = kernel_flops(w, materialised)
         res["kernels"] = {kname: {"ms": ms, "tflops": kf[kname] / ms / 1e9,
                                   "pct_peak": 100.0 * kf[kname] / ms / 1e9 / PEAK_TFLOPS}
                           for kname, ms in per.items()}
@@ -203,7 +221,10 @@ def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd", 
     return res
 
 
-KERNEL_TAGS = {"fwd": "fwd_kernel", "dq": "bwd_dq_kernel", "dkv": "bwd_dkv_kernel"}
+# Kernel-name tags per timed stage (the dQ stage is bwd_dq_kernel in the recomputing backward and
+# bwd_dq_ds_kernel in the materialised one, whose dK/dV stage also runs delta_kernel).
+KERNEL_TAGS = {"fwd": ("fwd_kernel",), "dq": ("bwd_dq_kernel", "bwd_dq_ds_kernel"), "dkv": ("bwd_dkv_kernel",),
+               "delta": ("delta_kernel",)}
 PMC_COUNTERS = ("FETCH_SIZE", "WRITE_SIZE")  # KiB per dispatch, one counter per rocprofv3 pass
 
 
@@ -228,8 +249,7 @@ def pmc_child(name, calib_mib):
     o, lse = _forward(q, k, v, w["causal"], w["window"], scale, store_lse=True)
     bufs = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
             torch.empty(lse.shape, dtype=torch.float32, device=dev))
-    _backward(q, k, v, o, lse, do, w["causal"], w["window"], scale, stages=_lib.GFA_BWD_DQ, out=bufs)
-    _backward(q, k, v, o, lse, do, w["causal"], w["window"], scale, stages=_lib.GFA_BWD_DKV, out=bufs)
+    _backward(q, k, v, o, lse, do, w["causal"], w["window"], scale, out=bufs)  # every backward kernel once
     torch.cuda.synchronize()
     del q, k, v, do, o, lse, bufs
     src = torch.empty((calib_mib << 20) // 4, dtype=torch.float32, device=dev).normal_()
@@ -300,8 +320,8 @@ def measure_traffic(name, calib_mib=1024, timeout_s=180, keep_dir=None):
         factor = copy_known_kib / copy_kib if copy_kib > 0 else float("nan")
         out[f"{counter.lower()}_factor"] = factor
         out["copy_kernel"] = last
-        for kname, tag in KERNEL_TAGS.items():
-            hits = [v for kn, v in vals.items() if tag in kn and "reduce" not in kn]
+        for kname, tags in KERNEL_TAGS.items():
+            hits = [v for kn, v in vals.items() if any(t in kn for t in tags) and "reduce" not in kn]
             if not hits:
                 continue
             kib = sum(hits[0]) / len(hits[0])
@@ -525,7 +545,7 @@ def main(argv=None):
     if "kernels" in h:
         dom = max(h["kernels"], key=lambda kname: h["kernels"][kname]["ms"])
         kd = h["kernels"][dom]
-        kb = kernel_bytes(WORKLOADS[head])
+        kb = kernel_bytes(WORKLOADS[head], h.get("ds_store_bytes", 0))
         tk = (traffic or {}).get("kernels", {})
         for kname, ent in h["kernels"].items():
             ent["algorithmic_bytes"] = kb[kname]
@@ -537,7 +557,7 @@ def main(argv=None):
                     "traffic": kd.get("traffic_bytes"),
                     "algorithmic_bytes": kb[dom],
                     "ms_per_launch": round(kd["ms"], 4),
-                    "flops_per_launch": kernel_flops(WORKLOADS[head])[dom]}
+                    "flops_per_launch": kernel_flops(WORKLOADS[head], h.get("bwd_form") == "materialised")[dom]}
         if traffic:
             roofline["traffic_calibration"] = {k_: round(traffic[k_], 4) for k_ in ("fetch_size_factor",
                                                                                      "write_size_factor")

@@ -33,10 +33,10 @@ STATUS_NAMES = {
 # GFA_VERSION of include/gfa.h whose struct layouts FwdArgs / BwdArgs below mirror. A library
 # built from other sources reads another prefix of the argument structs (an older one ignores the
 # segment, soft-cap and dropout fields), so load() refuses it instead of computing wrong results.
-ABI_VERSION = 105
+ABI_VERSION = 106
 
-EXPORTED = ("gfa_fwd", "gfa_bwd", "gfa_bwd_noalloc", "gfa_bwd_workspace_size", "gfa_config", "gfa_last_error",
-            "gfa_version", "gfa_set_runtime_scheduling")
+EXPORTED = ("gfa_fwd", "gfa_bwd", "gfa_bwd_noalloc", "gfa_bwd_workspace_size", "gfa_bwd_workspace_bytes",
+            "gfa_bwd_ds_limit", "gfa_config", "gfa_last_error", "gfa_version", "gfa_set_runtime_scheduling")
 NOALLOC_SCRATCH_BYTES = 64 << 20  # GFA_NOALLOC_SCRATCH_BYTES
 
 
@@ -119,6 +119,10 @@ def load() -> ctypes.CDLL:
         lib.gfa_bwd_noalloc.restype = ctypes.c_int
         lib.gfa_bwd_workspace_size.argtypes = [ctypes.c_int32] * 8
         lib.gfa_bwd_workspace_size.restype = ctypes.c_size_t
+        lib.gfa_bwd_workspace_bytes.argtypes = [ctypes.POINTER(BwdArgs)]
+        lib.gfa_bwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.gfa_bwd_ds_limit.argtypes = [ctypes.c_int64]
+        lib.gfa_bwd_ds_limit.restype = ctypes.c_int64
         lib.gfa_config.argtypes = [ctypes.c_int32] * 5 + [ctypes.POINTER(ConfigInfo)]
         lib.gfa_config.restype = ctypes.c_int
         lib.gfa_last_error.argtypes = []
@@ -146,6 +150,16 @@ def set_runtime_scheduling(enable: bool) -> bool:
     """Switch the run-time work distribution of the head_dim-512 grids on or off (process-wide;
     results are bitwise the same either way). Returns the previous setting."""
     return bool(load().gfa_set_runtime_scheduling(1 if enable else 0))
+
+
+def set_bwd_ds_limit(nbytes: int) -> int:
+    """Largest dS store (bytes) the materialised backward may use; 0 switches that form off.
+    Process-wide; returns the previous limit."""
+    return int(load().gfa_bwd_ds_limit(int(nbytes)))
+
+
+def bwd_ds_limit() -> int:
+    return int(load().gfa_bwd_ds_limit(-1))
 
 
 def strides_of(t) -> Strides:

@@ -196,7 +196,9 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
               stages: int = 0, out=None, noalloc: bool = False, segments=None, softcap: float = 0.0,
               dropout_p: float = 0.0, dropout_seed: int = 0):
     """Run gfa_bwd. ``stages`` selects kernels (0 = all; GFA_BWD_DQ / GFA_BWD_DKV bits);
-    ``out`` = (dq, dk, dv, delta) reuses caller buffers (profiling a single stage).
+    ``out`` = (dq, dk, dv, delta) reuses caller buffers (profiling a single stage), and a fifth
+    entry, a uint8 tensor, is the workspace (for the materialised form a GFA_BWD_DQ call reads the
+    dS store a GFA_BWD_DKV call left there; it must hold gfa_bwd_workspace_bytes).
     ``noalloc`` calls gfa_bwd_noalloc instead: delta and the workspace then live in the
     library's own scratch (the returned delta is None)."""
     B, Hq, N, D = q.shape
@@ -204,8 +206,11 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
     do = _prep(do)
     if do.dtype != q.dtype:
         do = do.to(q.dtype)
+    ws = None
     if out is not None:
-        dq, dk, dv, delta = out
+        dq, dk, dv, delta = out[:4]
+        if len(out) > 4:
+            ws = out[4]
     else:
         dq = torch.empty_like(q)
         dk = torch.empty_like(k)
@@ -214,9 +219,6 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
                       for t in (dq, dk, dv))
         delta = None if noalloc else torch.empty((B, Hq, lse_ld(N)), dtype=torch.float32, device=q.device)
     lib = _lib.load()
-    ws_bytes = 0 if noalloc else int(lib.gfa_bwd_workspace_size(B, Hq, Hkv, N, D, int(bool(causal)), int(slide_size),
-                                                                 int(q_splits)))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     a = _lib.BwdArgs()
     a.q, a.k, a.v, a.o, a.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr()
     a.lse, a.delta = lse.data_ptr(), (delta.data_ptr() if delta is not None else None)
@@ -231,16 +233,38 @@ def _backward(q, k, v, o, lse, do, causal: bool, slide_size: int, scale: float, 
     a.q_splits = int(q_splits)
     a.lse_ld = lse.shape[-1]
     a.stages = int(stages)
-    a.workspace = ws.data_ptr() if ws is not None else None
-    a.workspace_bytes = ws_bytes
     a.softcap = float(softcap)
     a.dropout_p, a.dropout_seed = float(dropout_p), int(dropout_seed)
     a.stream = _stream(q.device)
     if segments is not None:
         a.seg_lo, a.seg_hi = segments[0].data_ptr(), segments[1].data_ptr()
+    if not noalloc:
+        need = int(lib.gfa_bwd_workspace_bytes(ctypes.byref(a)))
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need else None
+        a.workspace = ws.data_ptr() if ws is not None else None
+        a.workspace_bytes = ws.numel() if ws is not None else 0
     with torch.cuda.device(q.device):
         _lib.check((lib.gfa_bwd_noalloc if noalloc else lib.gfa_bwd)(ctypes.byref(a)))
     return dq, dk, dv, delta
+
+
+def backward_workspace(B: int, Hq: int, Hkv: int, N: int, D: int, causal: bool, slide_size: int, dtype=None,
+                       q_splits: int = 0, segments: bool = False, softcap: float = 0.0, dropout_p: float = 0.0):
+    """(bytes, materialised): the workspace gfa_bwd takes for this problem (gfa_bwd_workspace_bytes)
+    and whether it then runs the materialised backward (a delta kernel, dK/dV storing dS, dQ from
+    the store) rather than the recomputing one."""
+    lib = _lib.load()
+    a = _lib.BwdArgs()
+    a.batch, a.heads_q, a.heads_kv, a.seq_len, a.head_dim = B, Hq, Hkv, N, D
+    a.causal, a.window, a.q_splits = int(bool(causal)), int(slide_size), int(q_splits)
+    a.dtype = _DTYPES[dtype if dtype is not None else torch.bfloat16]
+    if segments:  # only the presence of a table matters for the size
+        a.seg_lo = a.seg_hi = 16
+    a.softcap, a.dropout_p = float(softcap), float(dropout_p)
+    need = int(lib.gfa_bwd_workspace_bytes(ctypes.byref(a)))
+    base = int(lib.gfa_bwd_workspace_size(B, Hq, Hkv, N, D, int(bool(causal)), int(slide_size), int(q_splits)))
+    return need, need > base
 
 
 def _default_scale(d: int, scale: float | None) -> float:

@@ -19,7 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libgfa.so")
-SOURCES = ["gfa_fwd.hip", "gfa_bwd_dq.hip", "gfa_bwd_dkv.hip", "gfa_api.hip"]
+SOURCES = ["gfa_fwd.hip", "gfa_bwd_dq.hip", "gfa_bwd_dkv.hip", "gfa_bwd_ds.hip", "gfa_api.hip"]
 ARCH = "gfx950"
 
 

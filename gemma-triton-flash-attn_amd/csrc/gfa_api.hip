@@ -411,7 +411,25 @@ namespace {
 // Validation and launches of the backward. `delta` and `ws` are the caller's buffers
 // (gfa_bwd) or slices of the library's scratch array (gfa_bwd_noalloc); `qs_in` is the
 // q_splits to use (0 = registry choice).
-int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_bytes, int qs_in) {
+// Materialised backward (gfa_ds.h): the byte size of the dS store of `a`, 0 when the problem
+// runs the recomputing form (store disabled or above the limit, segment tables, soft-capping,
+// dropout, or a dK/dV form without 64-key workgroups and a dQ-from-dS kernel).
+std::atomic<int64_t> g_ds_limit{int64_t(32) << 30};
+size_t ds_store_bytes(const gfa_bwd_args* a) {
+  const int64_t limit = g_ds_limit.load();
+  if (limit <= 0 || a->seg_lo != nullptr || a->softcap > 0.f || a->dropout_p > 0.f) return 0;
+  const bool win = is_windowed(a->causal, a->window, a->seq_len);
+  if (!(a->head_dim == 512 || (a->head_dim == 256 && win))) return 0;
+  const Entry* e = lookup(a->head_dim);
+  const DkvForm& f = dkv_form(e, a->causal, a->window, a->seq_len);
+  if (f.roles != 2 || f.waves != 4 || f.bq != 32) return 0;
+  const gfa::DsLayout l = gfa::ds_layout(a->seq_len, a->causal, win ? a->window : 0);
+  const size_t bytes = (size_t)a->batch * a->heads_q * (size_t)l.slab * 2048;
+  return bytes <= (size_t)limit ? bytes : 0;
+}
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_bytes, int qs_in, bool allow_ds) {
   int rc = check_dims(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->dtype, a->window);
   if (rc) return rc;
   if ((rc = check_view("q", a->q, a->q_strides, true))) return rc;
@@ -450,6 +468,10 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   if (need > 0 && (ws_buf == nullptr || ws_bytes < need))
     return fail(GFA_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, ws_bytes);
   if (need > 0 && !aligned16(ws_buf)) return fail(GFA_ERR_INVALID_ARGUMENT, "workspace is not 16-byte aligned");
+  // The materialised form when the caller's workspace also holds the dS store.
+  const size_t ds_bytes = allow_ds ? ds_store_bytes(a) : 0;
+  const size_t ds_off = align256(need);
+  const bool use_ds = ds_bytes > 0 && ws_buf != nullptr && aligned16(ws_buf) && ws_bytes >= ds_off + ds_bytes;
 
   const bool bf16 = a->dtype == GFA_DTYPE_BF16;
   const int R = a->heads_q / a->heads_kv;
@@ -488,12 +510,12 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   pq.lse_ld = a->lse_ld;
   pq.g = make_qgrid(pq.B, pq.Hkv, R, pq.N, e->dq_waves / e->dq_split);
   hipError_t err = hipSuccess;
-  if (stages & GFA_BWD_DQ) {
+  if (stages & GFA_BWD_DQ && !use_ds) {
     if ((rc = setup_queue(stream, a->head_dim, pq.g.nblocks, &pq.sched))) return rc;
     err = gfa::launch_bwd_dq(pq, a->head_dim, e->dq_bkv, e->dq_split, bf16, cap, drop, stream);
     if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dQ launch failed: %s", hipGetErrorString(err));
   }
-  if (!(stages & GFA_BWD_DKV)) return ok();
+  if (!(stages & GFA_BWD_DKV) && !use_ds) return ok();
 
   gfa::BwdDkvParams pk;
   pk.seg_lo = a->seg_lo;
@@ -534,6 +556,51 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   const int keys_per_wg = 32 * (f.waves / f.roles);
   pk.n_kb = (pk.N + keys_per_wg - 1) / keys_per_wg;
   pk.nblocks = (pk.n_kb + 3) / 4 * 4 * pk.B * pk.Hkv * qs;  // key blocks in groups of four (bwd_dkv_kernel)
+  pk.dsl = gfa::ds_layout(a->seq_len, a->causal, window);
+  pk.dsl.ds = use_ds ? reinterpret_cast<uint16_t*>(static_cast<char*>(ws_buf) + ds_off) : nullptr;
+  if (use_ds) {
+    // delta, dK/dV (storing dS), then dQ from the store; GFA_BWD_DKV runs the first two,
+    // GFA_BWD_DQ the last (reading the store a GFA_BWD_DKV call left in the same workspace).
+    if (stages & GFA_BWD_DKV) {
+      gfa::DeltaParams pd;
+      pd.o = pq.o;
+      pd.dout = pq.dout;
+      pd.delta = delta_buf;
+      pd.ov = pq.ov;
+      pd.dov = pq.dov;
+      pd.B = a->batch;
+      pd.Hq = a->heads_q;
+      pd.N = a->seq_len;
+      pd.D = a->head_dim;
+      pd.lse_ld = a->lse_ld;
+      err = gfa::launch_delta(pd, bf16, stream);
+      if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "delta launch failed: %s", hipGetErrorString(err));
+      err = gfa::launch_bwd_dkv(pk, a->head_dim, f.bq, f.waves, f.roles, bf16, cap, drop, stream);
+      if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV launch failed: %s", hipGetErrorString(err));
+      if (qs > 1) {
+        err = gfa::launch_dkv_reduce(pk, a->head_dim, bf16, stream);
+        if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV reduce launch failed: %s", hipGetErrorString(err));
+      }
+    }
+    if (stages & GFA_BWD_DQ) {
+      gfa::BwdDqDsParams pz;
+      pz.k = pq.k;
+      pz.dq = pq.dq;
+      pz.kv = pq.kv;
+      pz.dqv = pq.dqv;
+      pz.B = a->batch;
+      pz.Hq = a->heads_q;
+      pz.Hkv = a->heads_kv;
+      pz.N = a->seq_len;
+      pz.R = R;
+      pz.scale = a->scale;
+      pz.dsl = pk.dsl;
+      pz.g = make_qgrid(pz.B, pz.Hkv, R, pz.N, 4);
+      err = gfa::launch_bwd_dq_ds(pz, a->head_dim, bf16, stream);
+      if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dQ (from dS) launch failed: %s", hipGetErrorString(err));
+    }
+    return ok();
+  }
   err = gfa::launch_bwd_dkv(pk, a->head_dim, f.bq, f.waves, f.roles, bf16, cap, drop, stream);
   if (err != hipSuccess) return fail(GFA_ERR_LAUNCH, "dKV launch failed: %s", hipGetErrorString(err));
   if (qs > 1) {
@@ -587,9 +654,25 @@ int scratch_on(hipStream_t stream, void** out) {
 
 extern "C" {
 
+size_t gfa_bwd_workspace_bytes(const gfa_bwd_args* a) {
+  if (a == nullptr) return 0;
+  const Entry* e = lookup(a->head_dim);
+  if (e == nullptr || a->batch <= 0 || a->heads_kv <= 0 || a->seq_len <= 0) return 0;
+  const int qs = a->q_splits > 0 ? a->q_splits : pick_q_splits(e, a->batch, a->heads_kv, a->seq_len, a->causal, a->window);
+  const size_t need = gfa_bwd_workspace_size(a->batch, a->heads_q, a->heads_kv, a->seq_len, a->head_dim, a->causal,
+                                             a->window, qs);
+  const size_t ds = ds_store_bytes(a);
+  return ds > 0 ? align256(need) + ds : need;
+}
+
+int64_t gfa_bwd_ds_limit(int64_t bytes) {
+  if (bytes < 0) return g_ds_limit.load();
+  return g_ds_limit.exchange(bytes);
+}
+
 int gfa_bwd(const gfa_bwd_args* a) {
   if (a == nullptr) return fail(GFA_ERR_INVALID_ARGUMENT, "args is NULL");
-  return bwd_impl(a, a->delta, a->workspace, a->workspace_bytes, a->q_splits);
+  return bwd_impl(a, a->delta, a->workspace, a->workspace_bytes, a->q_splits, true);
 }
 
 int gfa_bwd_noalloc(const gfa_bwd_args* a) {
@@ -626,7 +709,7 @@ int gfa_bwd_noalloc(const gfa_bwd_args* a) {
   void* base = nullptr;
   if ((rc = scratch_on(static_cast<hipStream_t>(a->stream), &base))) return rc;
   char* p = static_cast<char*>(base);
-  return bwd_impl(a, reinterpret_cast<float*>(p), ws ? p + delta_bytes : nullptr, ws, qs);
+  return bwd_impl(a, reinterpret_cast<float*>(p), ws ? p + delta_bytes : nullptr, ws, qs, false);
 }
 
 }  // extern "C"

@@ -314,6 +314,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   }
 
   // P on the key lanes (rows = queries per register): exp2 against the row LSE, masked.
+
+  // The dS store (p.dsl.ds set): the lane's 16 bytes of part c (= 2 * half-of-the-queries + h;
+  // the lane's key l32, 8 queries) of the 32 x 32 block of query tile q0 / 32 and this pair's key
+  // unit, head r_cur of the group, so that one wave's store is 1 KB contiguous; see gfa_ds.h.
+  auto store_ds = [&](int q0, int c, const i16x8& v) __attribute__((always_inline)) {
+    if (p.dsl.ds != nullptr && active) {
+      const int64_t blk = ((int64_t)b * p.Hq + kvh * p.R + r_cur) * p.dsl.slab + ds_index(p.dsl, q0 / 32, k0 / 32);
+      // Non-temporal: the block is read once, by the dQ kernel, so it should not push the query
+      // tiles the key blocks share out of L2.
+      __builtin_nontemporal_store(v, reinterpret_cast<i16x8*>(p.dsl.ds + blk * 1024 + c * 256 + l32 * 8));
+    }
+  };
   // exps_done: sc already holds the exponentials (computed under the dP chain), only the mask is left.
   auto p_elem = [&](float sv, float lse) __attribute__((always_inline)) {
     return fast_exp2(sv * p.scale_log2 - lse * kLog2e);
@@ -540,6 +552,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
             }
             *reinterpret_cast<i16x8 GFA_LDS*>(slot(sb, RO == 0 ? 3 : 2, 0)) = give;
             pb_sh[sb * 2 + RO] = keep;
+            store_ds(q0 + sb * 32, 2 * RO + h, RO == 0 ? give : keep);
           }
           barrier_lds();  // the halves handed back are in the slots
   #pragma unroll
@@ -609,6 +622,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
         for (int i = 0; i < BQ / 16; ++i) pb[i] = pb_sh[i];
       } else {
         pack(s, pb);
+        if (role == 1) {
+#pragma unroll
+          for (int i = 0; i < BQ / 16; ++i) store_ds(q0 + (i >> 1) * 32, 2 * (i & 1) + h, pb[i]);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
@@ -719,9 +736,20 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     }
   };
 
+  // dS store: the stores this wave issues per tile, after that tile's copies of the next one.
+  // The tile barrier leaves them in flight (they complete in issue order, behind the copies).
+  const int nst_wave = (p.dsl.ds != nullptr && active) ? (SHARED ? 1 : (ROLES == 2 && role == 1 ? BQ / 16 : 0)) : 0;
   for (int it = it_lo; it < it_hi; ++it) {
     const int cur = (it - it_lo) & 1;
-    barrier_tile();  // tile `it` landed; every wave is done with the other buffers and px
+    // tile `it` landed; every wave is done with the other buffers and px
+    const int nst = it == it_lo ? 0 : nst_wave;
+    if (nst == 0) {
+      barrier_tile();
+    } else if (nst == 1) {
+      barrier_tile_n<1>();
+    } else {
+      barrier_tile_n<BQ / 16>();
+    }
     const int q0 = qt_c * BQ;
     // Row statistics of this tile (rows q0 + sb*32 + 8g + 4h + 0..3; rows padded to a
     // multiple of 64), issued before the prefetch so they are not queued behind it.

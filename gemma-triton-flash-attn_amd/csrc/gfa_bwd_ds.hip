@@ -1,0 +1,259 @@
+// GQA flash-attention backward, materialised form: the delta kernel and dQ from the dS store.
+//
+// Same results as /root/reference/flash_attn/attention.py:687-797 (dQ kernel, STORE_DELTA=True),
+// by another decomposition. The dK/dV kernel (gfa_bwd_dkv.hip) computes dS = P (dP - delta) for
+// every 32 x 32 block it visits anyway; in this form it also stores that block, rounded to the
+// input dtype (the reference rounds dS there too, attention.py:791, before dS K). dQ is then one
+// product per block, dQ = scale * dS K (attention.py:791-797), instead of the three of the
+// recomputing kernel (S, dP and dS K): a third of its matrix work, for 2 KB of dS per block read
+// from HBM. Delta = rowsum(dO O) (attention.py:733-744), which the recomputing dQ kernel
+// produces in its prologue, comes from its own small kernel ahead of dK/dV.
+#include "gfa_common.h"
+#include "gfa_params.h"
+#include "gfa_launch.h"
+
+namespace gfa {
+
+// One workgroup per 32 rows of one (batch, head): each row's 16-byte chunks spread over the
+// lanes of one wave (whole rows per instruction, coalesced), partial products summed across
+// those lanes. Rows past N repeat row N - 1, as the recomputing dQ kernel writes them.
+template <int D, bool IS_BF16>
+__global__ __launch_bounds__(256) void delta_kernel(const DeltaParams p) {
+  constexpr int CPR = D / 8;     // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;  // rows per wave and instruction
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int bh = blockIdx.y;  // b * Hq + head
+  const int b = bh / p.Hq, head = bh % p.Hq;
+  const uint16_t* ob = p.o + (int64_t)b * p.ov.sb + (int64_t)head * p.ov.sh;
+  const uint16_t* db = p.dout + (int64_t)b * p.dov.sb + (int64_t)head * p.dov.sh;
+  const int lc = lane % CPR;
+#pragma unroll
+  for (int it = 0; it < 32 / (4 * RPI); ++it) {
+    const int row = blockIdx.x * 32 + (it * 4 + wave) * RPI + lane / CPR;
+    const int r = min(row, p.N - 1);
+    const i16x8 o = *reinterpret_cast<const i16x8*>(ob + (int64_t)r * p.ov.sn + 8 * lc);
+    const i16x8 d = *reinterpret_cast<const i16x8*>(db + (int64_t)r * p.dov.sn + 8 * lc);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += from16<IS_BF16>(d[e]) * from16<IS_BF16>(o[e]);
+#pragma unroll
+    for (int m = CPR / 2; m >= 1; m >>= 1) s += __shfl_xor(s, m, CPR);
+    if (lc == 0) p.delta[(int64_t)bh * p.lse_ld + row] = s;
+  }
+}
+
+// dQ from the dS store. A workgroup is four waves, each one (head, 32-row query tile) of one KV
+// head (the QGrid split of the forward). The waves share the K tiles, in a ring of three LDS
+// buffers filled by direct global->LDS copies two tiles ahead; each wave copies its own 2 KB dS
+// block of the tile next to them (the blocks come from HBM, further away than a tile step). Per tile and wave: dQ^T += K^T dS^T, two k-steps of 16 keys, A operands read transposed
+// from the K tile (as in the recomputing kernel), B operands read transposed from the dS block:
+// lane n gets the query sigma(n) of the block layout (gfa_ds.h), which is the query its
+// accumulator column belongs to. A wave skips the products of tiles outside its own row of blocks
+// (the workgroup's range is the union of its waves').
+template <int D, bool IS_BF16, int WPE>
+__global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams p) {
+  constexpr int NW = 4;
+  constexpr int BKV = 32;
+  constexpr int TILE = BKV * D * 2;
+  constexpr int DB = D / 32;
+  constexpr int DSB = 2048;  // one dS block
+  // Distinct LDS objects (the loop is unrolled by three, so every access names its buffer and
+  // the compiler's wait insertion can tell the reads from the copies in flight).
+  __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
+  __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
+  __shared__ __attribute__((aligned(1024))) char k_lds2[TILE];
+  __shared__ __attribute__((aligned(1024))) char s_lds0[NW * DSB];
+  __shared__ __attribute__((aligned(1024))) char s_lds1[NW * DSB];
+  __shared__ __attribute__((aligned(1024))) char s_lds2[NW * DSB];
+  char GFA_LDS* const K0 = (char GFA_LDS*)k_lds0;
+  char GFA_LDS* const K1 = (char GFA_LDS*)k_lds1;
+  char GFA_LDS* const K2 = (char GFA_LDS*)k_lds2;
+  char GFA_LDS* const S0 = (char GFA_LDS*)s_lds0;
+  char GFA_LDS* const S1 = (char GFA_LDS*)s_lds1;
+  char GFA_LDS* const S2 = (char GFA_LDS*)s_lds2;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = lane >> 5;
+  const int l32 = lane & 31;
+
+  int lid = xcd_remap((int)blockIdx.x, p.g.nblocks, p.g.n_hg);
+  const int hg = lid % p.g.n_hg;
+  lid /= p.g.n_hg;
+  const int kvh = lid % p.Hkv;
+  lid /= p.Hkv;
+  const int b = lid % p.B;
+  lid /= p.B;
+  // Full causal: longest rows first. Sliding window: the short first blocks first.
+  const int qsb = p.dsl.mode == 1 ? (p.g.n_qsb - 1 - lid) : lid;
+  const int head = kvh * p.R + hg * p.g.hpw + (wave % p.g.hpw);
+  const int qt = qsb * p.g.qbw + wave / p.g.hpw;  // this wave's query tile
+  const int q0 = qt * 32;
+  const bool active = q0 < p.N;
+
+  // Tile range: the union of the workgroup's rows of blocks (jmin and jmax do not decrease
+  // with the query tile), made a multiple of three (the loop is unrolled by three); the wave's
+  // own row.
+  const int wg_qt_lo = qsb * p.g.qbw;
+  const int wg_qt_last = min(p.dsl.nq, wg_qt_lo + p.g.qbw) - 1;
+  const int t_lo = ds_jmin(p.dsl, wg_qt_lo);
+  const int t_last = ds_jmax(p.dsl, wg_qt_last);
+  const int t_hi = t_lo + (t_last + 1 - t_lo + 2) / 3 * 3;
+  const int jlo = active ? ds_jmin(p.dsl, qt) : 1;
+  const int jhi = active ? ds_jmax(p.dsl, qt) : 0;
+
+  TileLoader<D, BKV, NW> kload;
+  kload.init(p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh, p.kv.sn, p.N, wave, lane);
+  const uint16_t* slab = p.dsl.ds + ((int64_t)b * p.Hq + head) * p.dsl.slab * 1024;
+  // The wave's dS block of unit j into its slot of sbuf: two 1 KB whole-wave copies, always
+  // issued (a block outside the wave's row reads through an empty buffer resource, which
+  // returns zeros and touches no memory), so every step issues the same number of copies and
+  // the tile barrier can count them.
+  constexpr int NI = TileLoader<D, BKV, NW>::NI;  // K tile copy instructions per wave
+  auto copy_ds = [&](int j, char GFA_LDS* sbuf) __attribute__((always_inline)) {
+    const bool mine = jlo <= j && j <= jhi;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(slab + (mine ? ds_index(p.dsl, qt, j) * 1024 : 0)), 0, mine ? DSB : 0, 0x00020000);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void GFA_LDS*)(sbuf + wave * DSB + c * 1024), 16, lane * 16,
+                                               c * 1024, 0, 2 /* nt: read once */);
+  };
+
+  // Transposed-read offsets: K tile (A operands, rows = keys 4h + t/4 and 8 further, swizzled
+  // chunks) and dS block (B operands, rows = keys at 16 bytes inside each 512-byte part).
+  int toffA[4], toffB[4];
+  int soffA, soffB;
+  {
+    const int t16 = lane & 15;
+    const int half16 = (lane >> 4) & 1;
+    const int rA = 4 * h + (t16 >> 2);
+    const int rB = rA + 8;
+#pragma unroll
+    for (int dl = 0; dl < 4; ++dl) {
+      const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
+      toffA[dl] = rA * (2 * D) + ((c ^ swz<D>(rA)) << 4) + (t16 & 1) * 8;
+      toffB[dl] = rB * (2 * D) + ((c ^ swz<D>(rB)) << 4) + (t16 & 1) * 8;
+    }
+    // part c = 2 half16 + ((t16 >> 1) & 1) (columns 8 c ..), 16-byte rows inside a part
+    const int sc = ((2 * half16 + ((t16 >> 1) & 1)) << 9) + (t16 & 1) * 8;
+    soffA = rA * 16 + sc;
+    soffB = rB * 16 + sc;
+  }
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
+
+  // kn, sn: the buffers of tile t + 2 (those of tile t - 1, which every wave has read once it is
+  // past this step's barrier).
+  auto step = [&](int t, const char GFA_LDS* kt, const char GFA_LDS* st, char GFA_LDS* kn, char GFA_LDS* sn)
+                  __attribute__((always_inline)) {
+    // Tile t landed (the wave's NI + 2 most recent copies, of tile t + 1, may still be in
+    // flight); every wave is done reading tile t - 1.
+    barrier_tile_n<NI + 2>();
+    // Past the end: the last tile's K again (never read) and empty dS copies.
+    kload.load(min(t + 2, t_hi - 1) * BKV, kn);
+    copy_ds(t + 2, sn);
+    if (jlo <= t && t <= jhi) {
+      i16x8 dsb[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) dsb[ks] = tr_frag(st + wave * DSB, soffA, soffB, ks * 256);
+      // Own scheduling region for the products: the read-ahead pattern of mma_tr_accumulate
+      // counts its own fragment reads only.
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (WPE > 1) __builtin_amdgcn_s_setprio(1);
+      mma_tr_accumulate<IS_BF16, D, DB, 2, 2, 1>(acc, kt, toffA, toffB, dsb);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (WPE > 1) __builtin_amdgcn_s_setprio(0);
+    }
+    if constexpr (WPE == 1) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
+    }
+  };
+
+  if (t_lo < t_hi) {
+    kload.load(t_lo * BKV, K0);
+    copy_ds(t_lo, S0);
+    kload.load(min(t_lo + 1, t_hi - 1) * BKV, K1);
+    copy_ds(t_lo + 1, S1);
+  }
+  for (int t = t_lo; t < t_hi; t += 3) {
+    step(t, K0, S0, K2, S2);
+    __builtin_amdgcn_sched_barrier(0);
+    step(t + 1, K1, S1, K0, S0);
+    __builtin_amdgcn_sched_barrier(0);
+    step(t + 2, K2, S2, K1, S1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  drain_tile_copies();
+
+  // Column l32 of the accumulators is query sigma(l32) of the tile; rows are head-dim
+  // elements 32 db + 8 g + 4 h + 0..3.
+  const int c8 = l32 >> 3, e8 = l32 & 7;
+  const int q = q0 + 16 * (c8 >> 1) + 8 * (e8 >> 2) + 4 * (c8 & 1) + (e8 & 3);
+  if (active && q < p.N) {
+    uint16_t* dqrow = p.dq + (int64_t)b * p.dqv.sb + (int64_t)head * p.dqv.sh + (int64_t)q * p.dqv.sn;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        i16x4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[db][4 * g + e] * p.scale);
+        *reinterpret_cast<i16x4*>(dqrow + db * 32 + 8 * g + 4 * h) = o4;
+      }
+    }
+  }
+}
+
+#define GFA_DS_INST(DD, WW)                                                                   \
+  template __global__ void bwd_dq_ds_kernel<DD, true, WW>(const BwdDqDsParams);               \
+  template __global__ void bwd_dq_ds_kernel<DD, false, WW>(const BwdDqDsParams);              \
+  template __global__ void delta_kernel<DD, true>(const DeltaParams);                         \
+  template __global__ void delta_kernel<DD, false>(const DeltaParams);
+GFA_DS_INST(512, 1)
+GFA_DS_INST(256, 2)
+#undef GFA_DS_INST
+
+hipError_t launch_delta(const DeltaParams& p, bool bf16, hipStream_t stream) {
+  const dim3 grid((p.N + 31) / 32, p.B * p.Hq);
+#define GFA_DELTA_CASE(DD)                                                                              \
+  if (p.D == DD) {                                                                                      \
+    if (bf16) {                                                                                         \
+      hipLaunchKernelGGL((delta_kernel<DD, true>), grid, dim3(256), 0, stream, p);                    \
+    } else {                                                                                            \
+      hipLaunchKernelGGL((delta_kernel<DD, false>), grid, dim3(256), 0, stream, p);                   \
+    }                                                                                                   \
+    return hipGetLastError();                                                                           \
+  }
+  GFA_DELTA_CASE(512)
+  GFA_DELTA_CASE(256)
+#undef GFA_DELTA_CASE
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_bwd_dq_ds(const BwdDqDsParams& p, int head_dim, bool bf16, hipStream_t stream) {
+  const dim3 grid(p.g.nblocks);
+  if (head_dim == 512) {
+    if (bf16) {
+      hipLaunchKernelGGL((bwd_dq_ds_kernel<512, true, 1>), grid, dim3(256), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((bwd_dq_ds_kernel<512, false, 1>), grid, dim3(256), 0, stream, p);
+    }
+    return hipGetLastError();
+  }
+  if (head_dim == 256) {
+    if (bf16) {
+      hipLaunchKernelGGL((bwd_dq_ds_kernel<256, true, 2>), grid, dim3(256), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((bwd_dq_ds_kernel<256, false, 2>), grid, dim3(256), 0, stream, p);
+    }
+    return hipGetLastError();
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace gfa

@@ -192,6 +192,16 @@ __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(
 // LDS traffic has drained (lgkmcnt): afterwards the whole tile is visible to every wave.
 __device__ __forceinline__ void barrier_tile() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// barrier_tile leaving this wave's N most recent vector-memory operations outstanding (vmcnt
+// counts loads and stores and completes them in issue order): the tile is there when the N
+// operations the wave issued after its copies are stores (or prefetches of later tiles) that the
+// barrier need not wait for.
+template <int N>
+__device__ __forceinline__ void barrier_tile_n() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 // Wait for this wave's outstanding global->LDS copies (the last, redundant prefetch of a
 // tile loop) so none lands after the workgroup's LDS has been handed to another one.
 __device__ __forceinline__ void drain_tile_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

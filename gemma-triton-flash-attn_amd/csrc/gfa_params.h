@@ -3,6 +3,8 @@
 #pragma once
 #include <stdint.h>
 
+#include "gfa_ds.h"
+
 namespace gfa {
 
 // Row addressing of one (B, H, N, D) tensor: element (b, h, n, d) lives at
@@ -120,6 +122,29 @@ struct BwdDkvParams {
   int lse_ld;
   int n_kb;          // number of key blocks (each WKV keys wide)
   int nblocks;       // q_splits * B * Hkv * n_kb rounded up to whole groups of four key blocks
+  DsLayout dsl;      // dS store (dsl.ds null: none)
+};
+
+// delta = rowsum(dO * O) of every row of the 32-row tiles that cover N (rows past N repeat row
+// N - 1), for the materialised backward, whose dQ kernel no longer computes it.
+struct DeltaParams {
+  const uint16_t* o;
+  const uint16_t* dout;
+  float* delta;  // (B, Hq, lse_ld)
+  RowView ov, dov;
+  int B, Hq, N, D;
+  int lse_ld;
+};
+
+// dQ = scale * dS K from the dS store (the materialised backward).
+struct BwdDqDsParams {
+  const uint16_t* k;
+  uint16_t* dq;
+  RowView kv, dqv;
+  int B, Hq, Hkv, N, R;
+  float scale;
+  DsLayout dsl;
+  QGrid g;
 };
 
 }  // namespace gfa

@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define GFA_VERSION 105 /* 1.0.5: run-time work distribution (1.0.4: attention dropout, 1.0.3: soft-capping) */
+#define GFA_VERSION 106 /* 1.0.6: materialised backward (1.0.5: run-time work distribution, 1.0.4: attention dropout, 1.0.3: soft-capping) */
 
 typedef enum {
   GFA_DTYPE_FP16 = 0,
@@ -123,8 +123,13 @@ typedef struct {
   int32_t q_splits;       /* 0 = registry choice, else 1, 2, 4 or 8 */
   int32_t lse_ld;         /* row length of lse and delta (>= GFA_LSE_LD(seq_len)) */
   int32_t stages;         /* 0 = all; else bitwise OR of GFA_BWD_DQ and GFA_BWD_DKV (profiling:
-                             GFA_BWD_DKV alone reads the delta a previous GFA_BWD_DQ wrote) */
-  void* workspace;        /* >= gfa_bwd_workspace_size(...) bytes when q_splits > 1 */
+                             recomputing form: GFA_BWD_DKV alone reads the delta a previous
+                             GFA_BWD_DQ wrote; materialised form: GFA_BWD_DKV runs delta and dK/dV,
+                             GFA_BWD_DQ alone reads the dS store a previous GFA_BWD_DKV call left in
+                             the same workspace) */
+  void* workspace;        /* >= gfa_bwd_workspace_size(...) bytes when q_splits > 1; with
+                             gfa_bwd_workspace_bytes(args) bytes the call runs the materialised
+                             backward where that form exists */
   size_t workspace_bytes;
   void* stream;
   const int32_t* seg_lo;  /* the forward's segment table, or NULL */
@@ -152,7 +157,16 @@ typedef struct {
 /* Forward: O (and LSE unless lse == NULL). Returns a gfa_status. */
 int gfa_fwd(const gfa_fwd_args* args);
 
-/* Backward: delta, dQ, then dK/dV (summing Q-split fp32 partials when q_splits > 1). */
+/* Backward: delta, dQ, then dK/dV (summing Q-split fp32 partials when q_splits > 1).
+ * Two forms, the same results to rounding:
+ * - recomputing (the reference's, attention.py:1506-1620): the dQ kernel recomputes S, P and dP
+ *   and computes delta in its prologue, then the dK/dV kernel;
+ * - materialised: a delta kernel, the dK/dV kernel, which also stores every 32 x 32 block of dS
+ *   it computes (16-bit, in the workspace), then dQ = scale * dS K from that store. It replaces
+ *   two thirds of the dQ kernel's matrix work with 2 KiB of dS per block, written once and read
+ *   once. Runs when the workspace holds the store (gfa_bwd_workspace_bytes), the store is within
+ *   gfa_bwd_ds_limit, head_dim is 512, or 256 with a sliding window, and the problem has no
+ *   segment table, soft-cap or dropout; otherwise the recomputing form runs. */
 int gfa_bwd(const gfa_bwd_args* args);
 
 /* Bytes of the library-owned device scratch of gfa_bwd_noalloc, per GPU. */
@@ -172,9 +186,22 @@ int gfa_bwd(const gfa_bwd_args* args);
  * on one GPU (concurrent streams or threads) race. Otherwise as gfa_bwd. */
 int gfa_bwd_noalloc(const gfa_bwd_args* args);
 
-/* Workspace bytes gfa_bwd needs for the given problem and q_splits (0 = registry choice). */
+/* Workspace bytes gfa_bwd needs for the given problem and q_splits (0 = registry choice) in the
+ * recomputing form. */
 size_t gfa_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seq_len, int32_t head_dim,
                               int32_t causal, int32_t window, int32_t q_splits);
+
+/* Workspace bytes of gfa_bwd(args) (the workspace fields are not read): the Q-split partials,
+ * plus, where the materialised form applies, the dS store (batch * heads_q blocks of 2 KiB per
+ * stored 32 x 32 (query tile, key tile) pair: per batch entry about heads_q * seq_len^2 bytes
+ * under full causal masking, twice that without causal masking, 2 * heads_q * seq_len *
+ * (window + 96) bytes with a sliding window). No counterpart in the reference. */
+size_t gfa_bwd_workspace_bytes(const gfa_bwd_args* args);
+
+/* Largest dS store the materialised backward uses, in bytes (default 32 GiB); a larger problem
+ * runs the recomputing form, and 0 switches the materialised form off. A negative value only
+ * queries. Process-wide; returns the limit before the call. No counterpart in the reference. */
+int64_t gfa_bwd_ds_limit(int64_t bytes);
 
 /* Fill *out with the configuration used for this problem without a sliding window (with a
  * window shorter than the sequence, the forward at head_dim 128 runs 32-key tiles, and the

@@ -1,6 +1,7 @@
 """Shared test setup: repo root on sys.path, the ``gpu`` marker, seeded input helpers."""
 from __future__ import annotations
 
+import contextlib
 import os
 import sys
 
@@ -47,3 +48,16 @@ def make_inputs(B, Hq, Hkv, N, D, dtype, device, seed=0, scale=1.0, with_do=True
             t = t.to(device=device, dtype=dtype)
         out.append(t)
     return out
+
+
+@contextlib.contextmanager
+def recomputing():
+    """gfa_bwd in its recomputing form for the duration (the dS store limit at 0): the form of the
+    reference and of gfa_bwd_noalloc, whose kernels a bitwise comparison needs on both sides."""
+    from gemma_triton_flash_attn_amd import _lib
+
+    prev = _lib.set_bwd_ds_limit(0)
+    try:
+        yield
+    finally:
+        _lib.set_bwd_ds_limit(prev)

@@ -33,7 +33,7 @@ fake_pointers = pytest.mark.skipif(torch.cuda.is_available(),
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     text = open(HEADER).read()
-    declared = sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(gfa_\w+)\s*\(", text, re.M)))
+    declared = sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t|const char\*)\s+(gfa_\w+)\s*\(", text, re.M)))
     assert declared, "no declarations parsed"
     assert set(declared) == set(_lib.EXPORTED)
     for name in declared:

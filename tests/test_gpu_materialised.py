@@ -1,0 +1,112 @@
+"""The materialised backward (include/gfa.h: a delta kernel, dK/dV storing every 32 x 32 block of
+dS it computes, then dQ = scale * dS K from that store) against the recomputing one on the same
+inputs, and its host-side contract: the stage split through a persistent workspace, the store
+size limit, and the problems that keep the recomputing form. Both forms compute the same
+quantities with the same roundings of P and dS to the input dtype, so they agree to accumulation
+order (a few 1e-4 relative); the oracle comparisons of the other GPU tests run the default form,
+which is the materialised one wherever it applies.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import make_inputs, recomputing
+
+pytestmark = pytest.mark.gpu
+
+FORM_TOL = 2e-3  # relative, materialised against recomputing (measured: 1e-5 .. 2e-4)
+
+CASES = {
+    # name: B, Hq, Hkv, N, D, causal, window, dtype, q_splits
+    "d512_causal_gqa8": (1, 16, 2, 2048, 512, True, 0, torch.bfloat16, 0),
+    "d512_causal_ragged": (1, 8, 2, 3001, 512, True, 0, torch.bfloat16, 0),
+    "d512_noncausal_b2": (2, 8, 2, 700, 512, False, 0, torch.bfloat16, 0),
+    "d512_causal_fp16": (1, 8, 1, 1024, 512, True, 0, torch.float16, 0),
+    "d512_qsplit4": (1, 8, 1, 2048, 512, True, 0, torch.bfloat16, 4),
+    "d512_tiny": (1, 4, 1, 33, 512, True, 0, torch.bfloat16, 0),
+    "d256_swa1024": (1, 16, 8, 4096, 256, True, 1024, torch.bfloat16, 0),
+    "d256_swa700_ragged": (1, 16, 4, 3000, 256, True, 700, torch.bfloat16, 0),
+    "d256_swa31": (2, 8, 2, 517, 256, True, 31, torch.bfloat16, 0),
+    "d256_swa512_fp16": (1, 8, 1, 1500, 256, True, 512, torch.float16, 0),
+}
+
+
+def _rel(a, b):
+    return float(torch.linalg.vector_norm(a.float() - b.float()) / torch.linalg.vector_norm(b.float()))
+
+
+def _run(q, k, v, do, causal, window, q_splits, out=None, stages=0):
+    from gemma_triton_flash_attn_amd.attention import _backward, _forward
+
+    sc = q.shape[-1] ** -0.5
+    o, lse = _forward(q, k, v, causal, window, sc, store_lse=True)
+    res = _backward(q, k, v, o, lse, do, causal, window, sc, q_splits=q_splits, out=out, stages=stages)
+    torch.cuda.synchronize()
+    return res
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_materialised_matches_recomputing(name, device):
+    from gemma_triton_flash_attn_amd.attention import backward_workspace
+
+    B, Hq, Hkv, N, D, causal, window, dtype, qs = CASES[name]
+    print(f"case {name}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal} window={window} {dtype} "
+          f"q_splits={qs}", flush=True)
+    assert backward_workspace(B, Hq, Hkv, N, D, causal, window, dtype, q_splits=qs)[1], "expected the materialised form"
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, dtype, device, seed=N + Hq)
+    mat = _run(q, k, v, do, causal, window, qs)
+    with recomputing():
+        assert not backward_workspace(B, Hq, Hkv, N, D, causal, window, dtype, q_splits=qs)[1]
+        rec = _run(q, k, v, do, causal, window, qs)
+    for nm, a, b in zip(("dQ", "dK", "dV"), mat[:3], rec[:3]):
+        assert torch.isfinite(a).all(), nm
+        assert _rel(a, b) <= FORM_TOL, f"{nm}: {_rel(a, b):.3e}"
+    # delta: the same row sums in another order
+    assert float((mat[3][..., :N] - rec[3][..., :N]).abs().max()) <= 1e-3
+
+
+def test_stage_split_through_the_workspace_is_bitwise(device):
+    """GFA_BWD_DKV (delta and dK/dV, storing dS), then GFA_BWD_DQ reading the store the first call
+    left in the same workspace, equals the one-call backward bit for bit."""
+    from gemma_triton_flash_attn_amd import _lib
+    from gemma_triton_flash_attn_amd.attention import backward_workspace
+
+    B, Hq, Hkv, N, D = 1, 8, 2, 1500, 512
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, torch.bfloat16, device, seed=3)
+    full = _run(q, k, v, do, True, 0, 0)
+    nbytes, mat = backward_workspace(B, Hq, Hkv, N, D, True, 0)
+    assert mat
+    bufs = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(full[3]),
+            torch.empty(nbytes, dtype=torch.uint8, device=device))
+    _run(q, k, v, do, True, 0, 0, out=bufs, stages=_lib.GFA_BWD_DKV)
+    _run(q, k, v, do, True, 0, 0, out=bufs, stages=_lib.GFA_BWD_DQ)
+    for nm, a, b in zip(("dQ", "dK", "dV"), bufs[:3], full[:3]):
+        assert torch.equal(a, b), nm
+    assert torch.equal(bufs[3][..., :N], full[3][..., :N])
+
+
+def test_store_limit_selects_the_form(device):
+    """A store above the limit runs the recomputing form (bit for bit the limit-0 results); the
+    limit restored, the materialised one again."""
+    from gemma_triton_flash_attn_amd import _lib
+    from gemma_triton_flash_attn_amd.attention import backward_workspace
+
+    B, Hq, Hkv, N, D = 1, 8, 1, 1024, 512
+    nbytes, mat = backward_workspace(B, Hq, Hkv, N, D, True, 0)
+    assert mat and nbytes > 0
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, torch.bfloat16, device, seed=5)
+    with recomputing():
+        rec = _run(q, k, v, do, True, 0, 0)
+    store = nbytes - (_lib.bwd_workspace_size(B, Hq, Hkv, N, D, True, 0) + 255) // 256 * 256  # past the partials
+    prev = _lib.set_bwd_ds_limit(store - 1)
+    try:
+        assert not backward_workspace(B, Hq, Hkv, N, D, True, 0)[1]
+        small = _run(q, k, v, do, True, 0, 0)
+    finally:
+        _lib.set_bwd_ds_limit(prev)
+    for a, b in zip(small[:3], rec[:3]):
+        assert torch.equal(a, b)
+    mat_out = _run(q, k, v, do, True, 0, 0)
+    assert not torch.equal(mat_out[0], rec[0])  # the other form ran (dQ accumulates in another order)
+    assert _rel(mat_out[0], rec[0]) <= FORM_TOL
