@@ -43,21 +43,26 @@ __global__ __launch_bounds__(256) void delta_kernel(const DeltaParams p) {
   }
 }
 
-// dQ from the dS store. A workgroup is four waves, each one (head, 32-row query tile) of one KV
-// head (the QGrid split of the forward). The waves share the K tiles, in a ring of three LDS
-// buffers filled by direct global->LDS copies two tiles ahead; each wave copies its own 2 KB dS
-// block of the tile next to them (the blocks come from HBM, further away than a tile step). Per tile and wave: dQ^T += K^T dS^T, two k-steps of 16 keys, A operands read transposed
-// from the K tile (as in the recomputing kernel), B operands read transposed from the dS block:
-// lane n gets the query sigma(n) of the block layout (gfa_ds.h), which is the query its
-// accumulator column belongs to. A wave skips the products of tiles outside its own row of blocks
-// (the workgroup's range is the union of its waves').
+// dQ from the dS store. A workgroup is four waves and owns four (head, 32-row query tile) units of
+// one KV head (the QGrid split of the forward). Wave w accumulates units 2 (w >> 1) and
+// 2 (w >> 1) + 1 over head-dim half w & 1: every K^T fragment it reads from LDS feeds the
+// products of both units, half the LDS reads per product of one unit per wave (the accumulation
+// is bound by those reads). The waves share the K tiles, in a ring of three LDS buffers filled by
+// direct global->LDS copies two tiles ahead; wave w copies the 2 KB dS block of unit w next to
+// them (the blocks come from HBM, further away than a tile step). Per tile and wave:
+// dQ^T[half] += K^T[half] dS^T for both units, two k-steps of 16 keys, A operands read transposed
+// from the K tile (as in the recomputing kernel), B operands read transposed from the dS blocks:
+// lane n gets the query sigma(n) of the block layout (gfa_ds.h), the query of its accumulator
+// column. A unit's B operand is zero on tiles outside its own row of blocks (the workgroup's
+// range is the union of its units').
 template <int D, bool IS_BF16, int WPE>
 __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams p) {
   constexpr int NW = 4;
   constexpr int BKV = 32;
   constexpr int TILE = BKV * D * 2;
-  constexpr int DB = D / 32;
-  constexpr int DSB = 2048;  // one dS block
+  constexpr int DH = D / 2;     // head-dim half of one wave
+  constexpr int DBH = DH / 32;  // its 32-wide accumulator blocks
+  constexpr int DSB = 2048;     // one dS block
   // Distinct LDS objects (the loop is unrolled by three, so every access names its buffer and
   // the compiler's wait insertion can tell the reads from the copies in flight).
   __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
@@ -77,6 +82,8 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5;
   const int l32 = lane & 31;
+  const int dh = wave & 1;        // head-dim half
+  const int u0 = 2 * (wave >> 1);  // this wave's units u0, u0 + 1
 
   int lid = xcd_remap((int)blockIdx.x, p.g.nblocks, p.g.n_hg);
   const int hg = lid % p.g.n_hg;
@@ -87,34 +94,34 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
   lid /= p.B;
   // Full causal: longest rows first. Sliding window: the short first blocks first.
   const int qsb = p.dsl.mode == 1 ? (p.g.n_qsb - 1 - lid) : lid;
-  const int head = kvh * p.R + hg * p.g.hpw + (wave % p.g.hpw);
-  const int qt = qsb * p.g.qbw + wave / p.g.hpw;  // this wave's query tile
-  const int q0 = qt * 32;
-  const bool active = q0 < p.N;
+  auto head_of = [&](int u) __attribute__((always_inline)) { return kvh * p.R + hg * p.g.hpw + u % p.g.hpw; };
+  auto qt_of = [&](int u) __attribute__((always_inline)) { return qsb * p.g.qbw + u / p.g.hpw; };
+  // unit u's row of blocks [jlo, jhi] (empty past the last query tile)
+  auto jlo_of = [&](int u) __attribute__((always_inline)) { return qt_of(u) < p.dsl.nq ? ds_jmin(p.dsl, qt_of(u)) : 1; };
+  auto jhi_of = [&](int u) __attribute__((always_inline)) { return qt_of(u) < p.dsl.nq ? ds_jmax(p.dsl, qt_of(u)) : 0; };
 
   // Tile range: the union of the workgroup's rows of blocks (jmin and jmax do not decrease
-  // with the query tile), made a multiple of three (the loop is unrolled by three); the wave's
-  // own row.
+  // with the query tile), made a multiple of three (the loop is unrolled by three).
   const int wg_qt_lo = qsb * p.g.qbw;
   const int wg_qt_last = min(p.dsl.nq, wg_qt_lo + p.g.qbw) - 1;
   const int t_lo = ds_jmin(p.dsl, wg_qt_lo);
   const int t_last = ds_jmax(p.dsl, wg_qt_last);
   const int t_hi = t_lo + (t_last + 1 - t_lo + 2) / 3 * 3;
-  const int jlo = active ? ds_jmin(p.dsl, qt) : 1;
-  const int jhi = active ? ds_jmax(p.dsl, qt) : 0;
+  const int jlo0 = jlo_of(u0), jhi0 = jhi_of(u0), jlo1 = jlo_of(u0 + 1), jhi1 = jhi_of(u0 + 1);
 
   TileLoader<D, BKV, NW> kload;
   kload.init(p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh, p.kv.sn, p.N, wave, lane);
-  const uint16_t* slab = p.dsl.ds + ((int64_t)b * p.Hq + head) * p.dsl.slab * 1024;
-  // The wave's dS block of unit j into its slot of sbuf: two 1 KB whole-wave copies, always
-  // issued (a block outside the wave's row reads through an empty buffer resource, which
+  // The dS block of unit `wave` and unit j into its slot of sbuf: two 1 KB whole-wave copies,
+  // always issued (a block outside the unit's row reads through an empty buffer resource, which
   // returns zeros and touches no memory), so every step issues the same number of copies and
   // the tile barrier can count them.
   constexpr int NI = TileLoader<D, BKV, NW>::NI;  // K tile copy instructions per wave
+  const int cjlo = jlo_of(wave), cjhi = jhi_of(wave), cqt = qt_of(wave);
+  const uint16_t* slab = p.dsl.ds + ((int64_t)b * p.Hq + head_of(wave)) * p.dsl.slab * 1024;
   auto copy_ds = [&](int j, char GFA_LDS* sbuf) __attribute__((always_inline)) {
-    const bool mine = jlo <= j && j <= jhi;
+    const bool have = cjlo <= j && j <= cjhi;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(slab + (mine ? ds_index(p.dsl, qt, j) * 1024 : 0)), 0, mine ? DSB : 0, 0x00020000);
+        const_cast<uint16_t*>(slab + (have ? ds_index(p.dsl, cqt, j) * 1024 : 0)), 0, have ? DSB : 0, 0x00020000);
 #pragma unroll
     for (int c = 0; c < 2; ++c)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void GFA_LDS*)(sbuf + wave * DSB + c * 1024), 16, lane * 16,
@@ -122,7 +129,8 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
   };
 
   // Transposed-read offsets: K tile (A operands, rows = keys 4h + t/4 and 8 further, swizzled
-  // chunks) and dS block (B operands, rows = keys at 16 bytes inside each 512-byte part).
+  // chunks, this wave's head-dim half) and dS block (B operands, rows = keys at 16 bytes inside
+  // each 512-byte part).
   int toffA[4], toffB[4];
   int soffA, soffB;
   {
@@ -133,8 +141,8 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
 #pragma unroll
     for (int dl = 0; dl < 4; ++dl) {
       const int c = 4 * dl + 2 * half16 + ((t16 >> 1) & 1);
-      toffA[dl] = rA * (2 * D) + ((c ^ swz<D>(rA)) << 4) + (t16 & 1) * 8;
-      toffB[dl] = rB * (2 * D) + ((c ^ swz<D>(rB)) << 4) + (t16 & 1) * 8;
+      toffA[dl] = rA * (2 * D) + ((c ^ swz<D>(rA)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
+      toffB[dl] = rB * (2 * D) + ((c ^ swz<D>(rB)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
     }
     // part c = 2 half16 + ((t16 >> 1) & 1) (columns 8 c ..), 16-byte rows inside a part
     const int sc = ((2 * half16 + ((t16 >> 1) & 1)) << 9) + (t16 & 1) * 8;
@@ -142,9 +150,9 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
     soffB = rB * 16 + sc;
   }
 
-  f32x16 acc[DB];
+  f32x16 acc0[DBH], acc1[DBH];
 #pragma unroll
-  for (int i = 0; i < DB; ++i) acc[i] = f32x16{};
+  for (int i = 0; i < DBH; ++i) acc0[i] = acc1[i] = f32x16{};
 
   // kn, sn: the buffers of tile t + 2 (those of tile t - 1, which every wave has read once it is
   // past this step's barrier).
@@ -156,21 +164,52 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
     // Past the end: the last tile's K again (never read) and empty dS copies.
     kload.load(min(t + 2, t_hi - 1) * BKV, kn);
     copy_ds(t + 2, sn);
-    if (jlo <= t && t <= jhi) {
-      i16x8 dsb[2];
+    const bool in0 = jlo0 <= t && t <= jhi0, in1 = jlo1 <= t && t <= jhi1;
+    if (in0 || in1) {
+      i16x8 b0[2], b1[2];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) dsb[ks] = tr_frag(st + wave * DSB, soffA, soffB, ks * 256);
-      // Own scheduling region for the products: the read-ahead pattern of mma_tr_accumulate
-      // counts its own fragment reads only.
+      for (int ks = 0; ks < 2; ++ks) {
+        b0[ks] = tr_frag(st + u0 * DSB, soffA, soffB, ks * 256);
+        b1[ks] = tr_frag(st + (u0 + 1) * DSB, soffA, soffB, ks * 256);
+        if (!in0) b0[ks] = i16x8{};
+        if (!in1) b1[ks] = i16x8{};
+      }
+      // Own scheduling region for the products: a fixed read-ahead of PF A fragments, two
+      // transposing reads after each pair of products.
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (WPE > 1) __builtin_amdgcn_s_setprio(1);
-      mma_tr_accumulate<IS_BF16, D, DB, 2, 2, 1>(acc, kt, toffA, toffB, dsb);
+      constexpr int N = 2 * DBH, PF = 2;
+      auto frag = [&](int i) __attribute__((always_inline)) {
+        const int ks = i / DBH, db = i % DBH;
+        return tr_frag(kt, toffA[db & 3], toffB[db & 3], ks * 16 * (2 * D) + 256 * (db >> 2));
+      };
+      i16x8 a[PF];
+#pragma unroll
+      for (int i = 0; i < PF; ++i) a[i] = frag(i);
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int ks = i / DBH, db = i % DBH;
+        const i16x8 cur = a[i % PF];
+        if (i + PF < N) a[i % PF] = frag(i + PF);
+        acc0[db] = mma32<IS_BF16>(cur, b0[ks], acc0[db]);
+        acc1[db] = mma32<IS_BF16>(cur, b1[ks], acc1[db]);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);
+#pragma unroll
+      for (int i = 0; i < N - PF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * PF, 0);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (WPE > 1) __builtin_amdgcn_s_setprio(0);
     }
     if constexpr (WPE == 1) {
 #pragma unroll
-      for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
+      for (int db = 0; db < DBH; ++db) {
+        pin_agpr(acc0[db]);
+        pin_agpr(acc1[db]);
+      }
     }
   };
 
@@ -190,23 +229,28 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
   }
   drain_tile_copies();
 
-  // Column l32 of the accumulators is query sigma(l32) of the tile; rows are head-dim
-  // elements 32 db + 8 g + 4 h + 0..3.
+  // Column l32 of the accumulators is query sigma(l32) of the unit's tile; rows are head-dim
+  // elements DH dh + 32 db + 8 g + 4 h + 0..3.
   const int c8 = l32 >> 3, e8 = l32 & 7;
-  const int q = q0 + 16 * (c8 >> 1) + 8 * (e8 >> 2) + 4 * (c8 & 1) + (e8 & 3);
-  if (active && q < p.N) {
-    uint16_t* dqrow = p.dq + (int64_t)b * p.dqv.sb + (int64_t)head * p.dqv.sh + (int64_t)q * p.dqv.sn;
+  const int qoff = 16 * (c8 >> 1) + 8 * (e8 >> 2) + 4 * (c8 & 1) + (e8 & 3);
+  auto store = [&](int u, const f32x16 (&acc)[DBH]) __attribute__((always_inline)) {
+    const int q = qt_of(u) * 32 + qoff;
+    if (q < p.N) {
+      uint16_t* dqrow = p.dq + (int64_t)b * p.dqv.sb + (int64_t)head_of(u) * p.dqv.sh + (int64_t)q * p.dqv.sn + dh * DH;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
+      for (int db = 0; db < DBH; ++db) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        i16x4 o4;
+        for (int g = 0; g < 4; ++g) {
+          i16x4 o4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[db][4 * g + e] * p.scale);
-        *reinterpret_cast<i16x4*>(dqrow + db * 32 + 8 * g + 4 * h) = o4;
+          for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[db][4 * g + e] * p.scale);
+          *reinterpret_cast<i16x4*>(dqrow + db * 32 + 8 * g + 4 * h) = o4;
+        }
       }
     }
-  }
+  };
+  store(u0, acc0);
+  store(u0 + 1, acc1);
 }
 
 #define GFA_DS_INST(DD, WW)                                                                   \
