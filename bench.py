@@ -221,10 +221,11 @@ def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd", 
     return res
 
 
-# Kernel-name tags per timed stage (the dQ stage is bwd_dq_kernel in the recomputing backward and
-# bwd_dq_ds_kernel in the materialised one, whose dK/dV stage also runs delta_kernel).
-KERNEL_TAGS = {"fwd": ("fwd_kernel",), "dq": ("bwd_dq_kernel", "bwd_dq_ds_kernel"), "dkv": ("bwd_dkv_kernel",),
-               "delta": ("delta_kernel",)}
+# Kernel-name tags per timed stage: the dQ stage is bwd_dq_kernel in the recomputing backward and
+# bwd_dq_ds_kernel in the materialised one, whose dK/dV stage runs delta_kernel, then bwd_dkv_kernel
+# (a stage's traffic is the sum over its kernels, as its time is).
+KERNEL_TAGS = {"fwd": ("fwd_kernel",), "dq": ("bwd_dq_kernel", "bwd_dq_ds_kernel"),
+               "dkv": ("bwd_dkv_kernel", "delta_kernel")}
 PMC_COUNTERS = ("FETCH_SIZE", "WRITE_SIZE")  # KiB per dispatch, one counter per rocprofv3 pass
 
 
@@ -324,7 +325,7 @@ def measure_traffic(name, calib_mib=1024, timeout_s=180, keep_dir=None):
             hits = [v for kn, v in vals.items() if any(t in kn for t in tags) and "reduce" not in kn]
             if not hits:
                 continue
-            kib = sum(hits[0]) / len(hits[0])
+            kib = sum(sum(h) / len(h) for h in hits)
             ent = out["kernels"].setdefault(kname, {})
             ent[f"{counter.lower()}_kib_raw"] = kib
             ent[f"{counter.lower()}_bytes"] = kib * 1024.0 * factor
