@@ -67,8 +67,8 @@ typedef enum {
 #define GFA_LSE_LD(seq_len) ((((seq_len) + 63) / 64) * 64)
 
 /* gfa_bwd_args.stages bits */
-#define GFA_BWD_DQ 1  /* delta + dQ kernel */
-#define GFA_BWD_DKV 2 /* dK/dV kernel (+ Q-split reduction) */
+#define GFA_BWD_DQ 1  /* recomputing form: delta + dQ kernel; materialised: dQ from the dS store */
+#define GFA_BWD_DKV 2 /* dK/dV kernel (+ Q-split reduction); materialised: delta kernel, then dK/dV */
 
 /* Element strides (batch, head, row) of one 4-D tensor; the head-dim stride is 1. */
 typedef struct {
