@@ -318,12 +318,21 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // The dS store (p.dsl.ds set): the lane's 16 bytes of part c (= 2 * half-of-the-queries + h;
   // the lane's key l32, 8 queries) of the 32 x 32 block of query tile q0 / 32 and this pair's key
   // unit, head r_cur of the group, so that one wave's store is 1 KB contiguous; see gfa_ds.h.
+  // The block's address is kept incrementally by the tile loop (ds_now: the block of the tile being
+  // processed; one head further is one slab further), so the block-index formula runs only when
+  // the walk moves to another query tile. The store form has 32-row query tiles (BQ = 32).
+  const int64_t ds_slab_bytes = p.dsl.slab * 2048;
+  char* const ds_group = reinterpret_cast<char*>(p.dsl.ds) + ((int64_t)b * p.Hq + kvh * p.R) * ds_slab_bytes;
+  auto ds_block = [&](int r, int qt) __attribute__((always_inline)) {
+    return ds_group + r * ds_slab_bytes + ds_index(p.dsl, qt, k0 / 32) * 2048;
+  };
+  char* ds_now = nullptr;
   auto store_ds = [&](int q0, int c, const i16x8& v) __attribute__((always_inline)) {
+    (void)q0;
     if (p.dsl.ds != nullptr && active) {
-      const int64_t blk = ((int64_t)b * p.Hq + kvh * p.R + r_cur) * p.dsl.slab + ds_index(p.dsl, q0 / 32, k0 / 32);
       // Non-temporal: the block is read once, by the dQ kernel, so it should not push the query
       // tiles the key blocks share out of L2.
-      __builtin_nontemporal_store(v, reinterpret_cast<i16x8*>(p.dsl.ds + blk * 1024 + c * 256 + l32 * 8));
+      __builtin_nontemporal_store(v, reinterpret_cast<i16x8*>(ds_now + c * 512 + l32 * 16));
     }
   };
   // exps_done: sc already holds the exponentials (computed under the dP chain), only the mask is left.
@@ -739,6 +748,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
   // dS store: the stores this wave issues per tile, after that tile's copies of the next one.
   // The tile barrier leaves them in flight (they complete in issue order, behind the copies).
   const int nst_wave = (p.dsl.ds != nullptr && active) ? (SHARED ? 1 : (ROLES == 2 && role == 1 ? BQ / 16 : 0)) : 0;
+  static_assert(BQ == 32, "the dS store addresses 32-row query tiles");
+  char* ds_next = p.dsl.ds != nullptr ? ds_block(r_c, qt_c) : nullptr;  // block of tile (r_c, qt_c)
   for (int it = it_lo; it < it_hi; ++it) {
     const int cur = (it - it_lo) & 1;
     // tile `it` landed; every wave is done with the other buffers and px
@@ -781,6 +792,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     qload.rebase(q_kv + (int64_t)r_n * p.qv.sh, p.qv.sn, p.N);
     dload.rebase(d_kv + (int64_t)r_n * p.dov.sh, p.dov.sn, p.N);
     r_cur = r_c;
+    ds_now = ds_next;
+    if (p.dsl.ds != nullptr) ds_next = qt_n == qt_c && r_n == r_c + 1 ? ds_next + ds_slab_bytes : ds_block(r_n, qt_n);
     r_c = r_n;
     qt_c = qt_n;
     tile_step(smem + cur * TILE, smem + (2 + cur) * TILE, smem + (cur ^ 1) * TILE, smem + (2 + (cur ^ 1)) * TILE, px,
