@@ -63,20 +63,27 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
   constexpr int DH = D / 2;     // head-dim half of one wave
   constexpr int DBH = DH / 32;  // its 32-wide accumulator blocks
   constexpr int DSB = 2048;     // one dS block
-  // Distinct LDS objects (the loop is unrolled by three, so every access names its buffer and
-  // the compiler's wait insertion can tell the reads from the copies in flight).
+  // PAIRED (one workgroup per CU): a ring of four tile buffers and one barrier per two tiles;
+  // otherwise (two workgroups per CU) a ring of three and a barrier per tile.
+  constexpr bool PAIRED = WPE == 1;
+  // Distinct LDS objects (the loop is unrolled over the ring, so every access names its buffer
+  // and the compiler's wait insertion can tell the reads from the copies in flight).
   __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
   __shared__ __attribute__((aligned(1024))) char k_lds2[TILE];
+  __shared__ __attribute__((aligned(1024))) char k_lds3[PAIRED ? TILE : 16];
   __shared__ __attribute__((aligned(1024))) char s_lds0[NW * DSB];
   __shared__ __attribute__((aligned(1024))) char s_lds1[NW * DSB];
   __shared__ __attribute__((aligned(1024))) char s_lds2[NW * DSB];
+  __shared__ __attribute__((aligned(1024))) char s_lds3[PAIRED ? NW * DSB : 16];
   char GFA_LDS* const K0 = (char GFA_LDS*)k_lds0;
   char GFA_LDS* const K1 = (char GFA_LDS*)k_lds1;
   char GFA_LDS* const K2 = (char GFA_LDS*)k_lds2;
+  char GFA_LDS* const K3 = (char GFA_LDS*)k_lds3;
   char GFA_LDS* const S0 = (char GFA_LDS*)s_lds0;
   char GFA_LDS* const S1 = (char GFA_LDS*)s_lds1;
   char GFA_LDS* const S2 = (char GFA_LDS*)s_lds2;
+  char GFA_LDS* const S3 = (char GFA_LDS*)s_lds3;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -101,12 +108,13 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
   auto jhi_of = [&](int u) __attribute__((always_inline)) { return qt_of(u) < p.dsl.nq ? ds_jmax(p.dsl, qt_of(u)) : 0; };
 
   // Tile range: the union of the workgroup's rows of blocks (jmin and jmax do not decrease
-  // with the query tile), made a multiple of three (the loop is unrolled by three).
+  // with the query tile), made a multiple of the loop's unroll (four or three tiles).
+  constexpr int UNROLL = PAIRED ? 4 : 3;
   const int wg_qt_lo = qsb * p.g.qbw;
   const int wg_qt_last = min(p.dsl.nq, wg_qt_lo + p.g.qbw) - 1;
   const int t_lo = ds_jmin(p.dsl, wg_qt_lo);
   const int t_last = ds_jmax(p.dsl, wg_qt_last);
-  const int t_hi = t_lo + (t_last + 1 - t_lo + 2) / 3 * 3;
+  const int t_hi = t_lo + (t_last + 1 - t_lo + UNROLL - 1) / UNROLL * UNROLL;
   const int jlo0 = jlo_of(u0), jhi0 = jhi_of(u0), jlo1 = jlo_of(u0 + 1), jhi1 = jhi_of(u0 + 1);
 
   TileLoader<D, BKV, NW> kload;
@@ -116,16 +124,29 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
   // returns zeros and touches no memory), so every step issues the same number of copies and
   // the tile barrier can count them.
   constexpr int NI = TileLoader<D, BKV, NW>::NI;  // K tile copy instructions per wave
+  // Inside a row the block index grows by one per key unit: block j of the row is srow + j.
   const int cjlo = jlo_of(wave), cjhi = jhi_of(wave), cqt = qt_of(wave);
   const uint16_t* slab = p.dsl.ds + ((int64_t)b * p.Hq + head_of(wave)) * p.dsl.slab * 1024;
+  const int64_t srow = cjlo <= cjhi ? ds_index(p.dsl, cqt, cjlo) - cjlo : 0;
+  // In LDS the 16-byte key rows of part c sit at row r ^ 4c (part c of a block at 512 c): the
+  // transposing B reads of one 32-lane half, which span the four parts at the same rows, then fall
+  // in distinct banks (unswizzled, the parts 512 bytes apart share banks: 4-way conflicts). Lane L
+  // of copy instruction i writes row L & 31 of part 2 i + (L >> 5), so it fetches that part's row
+  // (L & 31) ^ 4 (2 i + (L >> 5)).
+  unsigned svoff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = 2 * i + (lane >> 5);
+    svoff[i] = (unsigned)(c * 512 + 16 * ((lane & 31) ^ (4 * c)));
+  }
   auto copy_ds = [&](int j, char GFA_LDS* sbuf) __attribute__((always_inline)) {
     const bool have = cjlo <= j && j <= cjhi;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(slab + (have ? ds_index(p.dsl, cqt, j) * 1024 : 0)), 0, have ? DSB : 0, 0x00020000);
+        const_cast<uint16_t*>(slab + (have ? (srow + j) * 1024 : 0)), 0, have ? DSB : 0, 0x00020000);
 #pragma unroll
     for (int c = 0; c < 2; ++c)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void GFA_LDS*)(sbuf + wave * DSB + c * 1024), 16, lane * 16,
-                                               c * 1024, 0, 2 /* nt: read once */);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void GFA_LDS*)(sbuf + wave * DSB + c * 1024), 16, svoff[c], 0, 0,
+                                               2 /* nt: read once */);
   };
 
   // Transposed-read offsets: K tile (A operands, rows = keys 4h + t/4 and 8 further, swizzled
@@ -144,26 +165,25 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
       toffA[dl] = rA * (2 * D) + ((c ^ swz<D>(rA)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
       toffB[dl] = rB * (2 * D) + ((c ^ swz<D>(rB)) << 4) + (t16 & 1) * 8 + dh * DH * 2;
     }
-    // part c = 2 half16 + ((t16 >> 1) & 1) (columns 8 c ..), 16-byte rows inside a part
-    const int sc = ((2 * half16 + ((t16 >> 1) & 1)) << 9) + (t16 & 1) * 8;
-    soffA = rA * 16 + sc;
-    soffB = rB * 16 + sc;
+    // part c = 2 half16 + ((t16 >> 1) & 1) (columns 8 c ..), 16-byte rows inside a part, row r at
+    // r ^ 4c (the copy's swizzle; the second k-step's rows, 16 further, keep it: 4c < 16)
+    const int c = 2 * half16 + ((t16 >> 1) & 1);
+    soffA = c * 512 + 16 * (rA ^ (4 * c)) + (t16 & 1) * 8;
+    soffB = c * 512 + 16 * (rB ^ (4 * c)) + (t16 & 1) * 8;
   }
 
   f32x16 acc0[DBH], acc1[DBH];
 #pragma unroll
   for (int i = 0; i < DBH; ++i) acc0[i] = acc1[i] = f32x16{};
 
-  // kn, sn: the buffers of tile t + 2 (those of tile t - 1, which every wave has read once it is
-  // past this step's barrier).
-  auto step = [&](int t, const char GFA_LDS* kt, const char GFA_LDS* st, char GFA_LDS* kn, char GFA_LDS* sn)
-                  __attribute__((always_inline)) {
-    // Tile t landed (the wave's NI + 2 most recent copies, of tile t + 1, may still be in
-    // flight); every wave is done reading tile t - 1.
-    barrier_tile_n<NI + 2>();
-    // Past the end: the last tile's K again (never read) and empty dS copies.
-    kload.load(min(t + 2, t_hi - 1) * BKV, kn);
-    copy_ds(t + 2, sn);
+  // Copies of tile t into kn, sn. Past the end: the last tile's K again (never read) and empty
+  // dS copies.
+  auto issue = [&](int t, char GFA_LDS* kn, char GFA_LDS* sn) __attribute__((always_inline)) {
+    kload.load(min(t, t_hi - 1) * BKV, kn);
+    copy_ds(t, sn);
+  };
+  // The products of tile t (landed, in kt and st).
+  auto compute = [&](int t, const char GFA_LDS* kt, const char GFA_LDS* st) __attribute__((always_inline)) {
     const bool in0 = jlo0 <= t && t <= jhi0, in1 = jlo1 <= t && t <= jhi1;
     if (in0 || in1) {
       i16x8 b0[2], b1[2];
@@ -213,19 +233,111 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
     }
   };
 
+  // The products of tiles t and t + 1 (both landed, in ka, sa and kb, sb) as one stream: the B
+  // operands of both tiles are read up front (a unit's block outside its row is zeros in LDS, its
+  // copy having read through an empty buffer resource), and the A read-ahead runs across the
+  // tile boundary. mid() (the next copies) is issued between the two tiles' products.
+  auto compute_pair = [&](int t, const char GFA_LDS* ka, const char GFA_LDS* sa, const char GFA_LDS* kb,
+                          const char GFA_LDS* sb, auto&& mid) __attribute__((always_inline)) {
+    const bool on = (jlo0 <= t + 1 && t <= jhi0) || (jlo1 <= t + 1 && t <= jhi1);
+    constexpr int N = 2 * DBH, PF = 2;
+    auto frag = [&](const char GFA_LDS* kt, int i) __attribute__((always_inline)) {
+      const int ks = i / DBH, db = i % DBH;
+      return tr_frag(kt, toffA[db & 3], toffB[db & 3], ks * 16 * (2 * D) + 256 * (db >> 2));
+    };
+    i16x8 b0[2][2], b1[2][2], a[PF];
+    if (on) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        b0[0][ks] = tr_frag(sa + u0 * DSB, soffA, soffB, ks * 256);
+        b1[0][ks] = tr_frag(sa + (u0 + 1) * DSB, soffA, soffB, ks * 256);
+      }
+#pragma unroll
+      for (int i = 0; i < PF; ++i) a[i] = frag(ka, i);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        b0[1][ks] = tr_frag(sb + u0 * DSB, soffA, soffB, ks * 256);
+        b1[1][ks] = tr_frag(sb + (u0 + 1) * DSB, soffA, soffB, ks * 256);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int ks = i / DBH, db = i % DBH;
+        const i16x8 cur = a[i % PF];
+        a[i % PF] = i + PF < N ? frag(ka, i + PF) : frag(kb, i + PF - N);
+        acc0[db] = mma32<IS_BF16>(cur, b0[0][ks], acc0[db]);
+        acc1[db] = mma32<IS_BF16>(cur, b1[0][ks], acc1[db]);
+      }
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    mid();
+    if (on) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int ks = i / DBH, db = i % DBH;
+        const i16x8 cur = a[i % PF];
+        if (i + PF < N) a[i % PF] = frag(kb, i + PF);
+        acc0[db] = mma32<IS_BF16>(cur, b0[1][ks], acc0[db]);
+        acc1[db] = mma32<IS_BF16>(cur, b1[1][ks], acc1[db]);
+      }
+#pragma unroll
+      for (int i = 0; i < N - PF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * PF, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int db = 0; db < DBH; ++db) {
+      pin_agpr(acc0[db]);
+      pin_agpr(acc1[db]);
+    }
+  };
+
+  // A step of the three-buffer ring: tile t landed (the wave's NI + 2 most recent copies, of
+  // tile t + 1, may still be in flight) and every wave is done reading tile t - 1, whose buffers
+  // kn, sn take tile t + 2.
+  auto step = [&](int t, const char GFA_LDS* kt, const char GFA_LDS* st, char GFA_LDS* kn, char GFA_LDS* sn)
+                  __attribute__((always_inline)) {
+    barrier_tile_n<NI + 2>();
+    issue(t + 2, kn, sn);
+    compute(t, kt, st);
+  };
+
   if (t_lo < t_hi) {
-    kload.load(t_lo * BKV, K0);
-    copy_ds(t_lo, S0);
-    kload.load(min(t_lo + 1, t_hi - 1) * BKV, K1);
-    copy_ds(t_lo + 1, S1);
+    issue(t_lo, K0, S0);
+    issue(t_lo + 1, K1, S1);
   }
-  for (int t = t_lo; t < t_hi; t += 3) {
-    step(t, K0, S0, K2, S2);
-    __builtin_amdgcn_sched_barrier(0);
-    step(t + 1, K1, S1, K0, S0);
-    __builtin_amdgcn_sched_barrier(0);
-    step(t + 2, K2, S2, K1, S1);
-    __builtin_amdgcn_sched_barrier(0);
+  if constexpr (PAIRED) {
+    // Tiles two at a time: past the barrier tiles t, t + 1 have landed and every wave is done
+    // with t - 2, t - 1, whose buffers take t + 2, t + 3 (each copy issued before the products
+    // of the tile two ahead of it).
+    for (int t = t_lo; t < t_hi; t += 4) {
+      barrier_tile();
+      issue(t + 2, K2, S2);
+      compute_pair(t, K0, S0, K1, S1, [&]() __attribute__((always_inline)) { issue(t + 3, K3, S3); });
+      __builtin_amdgcn_sched_barrier(0);
+      barrier_tile();
+      issue(t + 4, K0, S0);
+      compute_pair(t + 2, K2, S2, K3, S3, [&]() __attribute__((always_inline)) { issue(t + 5, K1, S1); });
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    for (int t = t_lo; t < t_hi; t += 3) {
+      step(t, K0, S0, K2, S2);
+      __builtin_amdgcn_sched_barrier(0);
+      step(t + 1, K1, S1, K0, S0);
+      __builtin_amdgcn_sched_barrier(0);
+      step(t + 2, K2, S2, K1, S1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   drain_tile_copies();
 
