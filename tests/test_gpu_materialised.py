@@ -25,6 +25,8 @@ CASES = {
     "d512_causal_fp16": (1, 8, 1, 1024, 512, True, 0, torch.float16, 0),
     "d512_qsplit4": (1, 8, 1, 2048, 512, True, 0, torch.bfloat16, 4),
     "d512_tiny": (1, 4, 1, 33, 512, True, 0, torch.bfloat16, 0),
+    "d512_swa700_ragged": (1, 8, 2, 2500, 512, True, 700, torch.bfloat16, 0),
+    "d512_swa100_fp16_b2": (2, 4, 1, 1100, 512, True, 100, torch.float16, 0),
     "d256_swa1024": (1, 16, 8, 4096, 256, True, 1024, torch.bfloat16, 0),
     "d256_swa700_ragged": (1, 16, 4, 3000, 256, True, 700, torch.bfloat16, 0),
     "d256_swa31": (2, 8, 2, 517, 256, True, 31, torch.bfloat16, 0),
