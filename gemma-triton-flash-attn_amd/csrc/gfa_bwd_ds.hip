@@ -46,15 +46,16 @@ __global__ __launch_bounds__(256) void delta_kernel(const DeltaParams p) {
 // dQ from the dS store. A workgroup is four waves and owns four (head, 32-row query tile) units of
 // one KV head (the QGrid split of the forward). Wave w accumulates units 2 (w >> 1) and
 // 2 (w >> 1) + 1 over head-dim half w & 1: every K^T fragment it reads from LDS feeds the
-// products of both units, half the LDS reads per product of one unit per wave (the accumulation
-// is bound by those reads). The waves share the K tiles, in a ring of three LDS buffers filled by
-// direct global->LDS copies two tiles ahead; wave w copies the 2 KB dS block of unit w next to
-// them (the blocks come from HBM, further away than a tile step). Per tile and wave:
+// products of both units, half the LDS reads per product of one unit per wave. The waves share
+// the K tiles, in a ring of LDS buffers filled by direct global->LDS copies two tiles ahead (four
+// buffers and one barrier per two tiles with one workgroup per CU, three and one per tile with
+// two); wave w copies the 2 KB dS block of unit w next to them (the blocks come from HBM,
+// further away than a tile step). Per tile and wave:
 // dQ^T[half] += K^T[half] dS^T for both units, two k-steps of 16 keys, A operands read transposed
 // from the K tile (as in the recomputing kernel), B operands read transposed from the dS blocks:
 // lane n gets the query sigma(n) of the block layout (gfa_ds.h), the query of its accumulator
 // column. A unit's B operand is zero on tiles outside its own row of blocks (the workgroup's
-// range is the union of its units').
+// range is the union of its units'; the block's LDS slot then holds the zeros of an empty copy).
 template <int D, bool IS_BF16, int WPE>
 __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams p) {
   constexpr int NW = 4;
