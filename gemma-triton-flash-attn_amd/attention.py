@@ -276,8 +276,9 @@ class FlashAttnGQAFunction(torch.autograd.Function):
 
     forward(q, k, v, causal, slide_size, scale=None, segments=None, softcap=None, dropout_p=0.0)
     -> O; saves q, k, v, O, the fp32 LSE (of the undropped probabilities), the segment tables and
-    the dropout seed drawn for this call. backward(dO) -> dQ, dK, dV via gfa_bwd (dQ kernel with
-    fused delta, then pack-GQA dKV), regenerating the same dropout mask from that seed.
+    the dropout seed drawn for this call. backward(dO) -> dQ, dK, dV via gfa_bwd (the materialised
+    form where it applies: delta, pack-GQA dKV storing dS, dQ from the store; else the dQ kernel
+    with fused delta, then pack-GQA dKV), regenerating the same dropout mask from that seed.
     """
 
     @staticmethod

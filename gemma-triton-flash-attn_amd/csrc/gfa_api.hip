@@ -69,6 +69,10 @@ bool is_windowed(int causal, int window, int N) { return causal && window > 0 &&
 const DkvForm& dkv_form(const Entry* e, int causal, int window, int N) {
   return is_windowed(causal, window, N) ? e->dkv_window : e->dkv;
 }
+// The form gfa_bwd launches: soft-capped and dropout instances exist for the default form only.
+const DkvForm& bwd_dkv_form(const Entry* e, const gfa_bwd_args* a) {
+  return (a->softcap > 0.f || a->dropout_p > 0.f) ? e->dkv : dkv_form(e, a->causal, a->window, a->seq_len);
+}
 
 const Entry* lookup(int d) {
   for (const Entry& e : kRegistry)
@@ -417,11 +421,13 @@ namespace {
 std::atomic<int64_t> g_ds_limit{int64_t(32) << 30};
 size_t ds_store_bytes(const gfa_bwd_args* a) {
   const int64_t limit = g_ds_limit.load();
-  if (limit <= 0 || a->seg_lo != nullptr || a->softcap > 0.f || a->dropout_p > 0.f) return 0;
+  // Segment tables trim the dK/dV kernel's query-tile ranges per key block, so not every block of
+  // the store's rows would be written; soft-capping and dropout are in the stored dS already.
+  if (limit <= 0 || a->seg_lo != nullptr) return 0;
   const bool win = is_windowed(a->causal, a->window, a->seq_len);
   if (!(a->head_dim == 512 || (a->head_dim == 256 && win))) return 0;
   const Entry* e = lookup(a->head_dim);
-  const DkvForm& f = dkv_form(e, a->causal, a->window, a->seq_len);
+  const DkvForm& f = bwd_dkv_form(e, a);  // the storing forms: the role pairs of 4 waves
   if (f.roles != 2 || f.waves != 4 || f.bq != 32) return 0;
   const gfa::DsLayout l = gfa::ds_layout(a->seq_len, a->causal, win ? a->window : 0);
   const size_t bytes = (size_t)a->batch * a->heads_q * (size_t)l.slab * 2048;
@@ -552,7 +558,7 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
   // Soft-capped problems run the plain-chain form: the windowed D=256 pair starts its chains
   // from the row statistics and keeps no raw score. The split count stays the shared rule's
   // (any split is exact), so the workspace size does not depend on the cap.
-  const DkvForm& f = (cap || drop) ? e->dkv : dkv_form(e, a->causal, a->window, a->seq_len);
+  const DkvForm& f = bwd_dkv_form(e, a);
   const int keys_per_wg = 32 * (f.waves / f.roles);
   pk.n_kb = (pk.N + keys_per_wg - 1) / keys_per_wg;
   pk.nblocks = (pk.n_kb + 3) / 4 * 4 * pk.B * pk.Hkv * qs;  // key blocks in groups of four (bwd_dkv_kernel)

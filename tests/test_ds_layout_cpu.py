@@ -111,9 +111,14 @@ def test_workspace_sizes_and_forms():
                  (1, 16, 2, 4096, 128, True, 1024), (1, 8, 8, 1024, 64, True, 0)):  # D=128, D=64
         assert not backward_workspace(*args)[1], args
     assert not backward_workspace(1, 16, 8, 4096, 256, True, 4096)[1]  # window >= N: full causal D=256
-    for kw in ({"segments": True}, {"softcap": 30.0}, {"dropout_p": 0.1}):
-        nb, m = backward_workspace(1, 8, 1, 2048, 512, True, 0, **kw)
-        assert not m and nb == _lib.bwd_workspace_size(1, 8, 1, 2048, 512, True, 0), kw
+    nb, m = backward_workspace(1, 8, 1, 2048, 512, True, 0, segments=True)  # segment tables: recomputing
+    assert not m and nb == _lib.bwd_workspace_size(1, 8, 1, 2048, 512, True, 0)
+    for kw in ({"softcap": 30.0}, {"dropout_p": 0.1}):
+        assert backward_workspace(1, 8, 1, 2048, 512, True, 0, **kw)[1], kw  # in the stored dS
+        assert backward_workspace(1, 8, 1, 2048, 512, True, 500, **kw)[1], kw
+        # windowed D=256: their instances are the one-wave dK/dV form, which stores nothing
+        nb, m = backward_workspace(1, 16, 8, 4096, 256, True, 1024, **kw)
+        assert not m and nb == _lib.bwd_workspace_size(1, 16, 8, 4096, 256, True, 1024), kw
     prev = _lib.set_bwd_ds_limit(0)
     try:
         assert _lib.bwd_ds_limit() == 0

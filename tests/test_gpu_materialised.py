@@ -1,7 +1,7 @@
 """The materialised backward (include/gfa.h: a delta kernel, dK/dV storing every 32 x 32 block of
 dS it computes, then dQ = scale * dS K from that store) against the recomputing one on the same
 inputs, and its host-side contract: the stage split through a persistent workspace, the store
-size limit, and the problems that keep the recomputing form. Both forms compute the same
+size limit, and soft-capping and dropout in the materialised form. Both forms compute the same
 quantities with the same roundings of P and dS to the input dtype, so they agree to accumulation
 order (a few 1e-4 relative); the oracle comparisons of the other GPU tests run the default form,
 which is the materialised one wherever it applies.
@@ -46,6 +46,44 @@ def _run(q, k, v, do, causal, window, q_splits, out=None, stages=0):
     res = _backward(q, k, v, o, lse, do, causal, window, sc, q_splits=q_splits, out=out, stages=stages)
     torch.cuda.synchronize()
     return res
+
+
+FEATURE_CASES = {
+    # name: B, Hq, Hkv, N, D, causal, window, dtype, softcap, dropout_p
+    "d512_softcap30": (1, 8, 1, 1500, 512, True, 0, torch.bfloat16, 30.0, 0.0),
+    "d512_dropout": (1, 8, 2, 1024, 512, True, 0, torch.bfloat16, 0.0, 0.1),
+    "d512_swa700_softcap50_fp16": (1, 8, 2, 3000, 512, True, 700, torch.float16, 50.0, 0.0),
+    "d512_swa512_dropout_b2": (2, 4, 1, 1500, 512, True, 512, torch.bfloat16, 0.0, 0.15),
+}
+
+
+@pytest.mark.parametrize("name", list(FEATURE_CASES))
+def test_materialised_softcap_dropout(name, device):
+    """Soft-capping and dropout take the materialised form too at D=512 (the dK/dV kernel's
+    stored dS carries the soft-cap factor 1 - t^2 and the dropped dP); against the recomputing
+    form. (At D=256 their dK/dV instances are the one-wave form, which stores nothing: recomputing.)"""
+    from gemma_triton_flash_attn_amd.attention import _backward, _forward, backward_workspace
+
+    B, Hq, Hkv, N, D, causal, window, dtype, cap, dp = FEATURE_CASES[name]
+    print(f"case {name}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} window={window} {dtype} softcap={cap} "
+          f"dropout={dp}", flush=True)
+    assert backward_workspace(B, Hq, Hkv, N, D, causal, window, dtype, softcap=cap, dropout_p=dp)[1]
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, dtype, device, seed=N + 7)
+    sc = D ** -0.5
+    kw = dict(softcap=cap, dropout_p=dp, dropout_seed=1234)
+    o, lse = _forward(q, k, v, causal, window, sc, store_lse=True, **kw)
+
+    def bwd():
+        r = _backward(q, k, v, o, lse, do, causal, window, sc, **kw)
+        torch.cuda.synchronize()
+        return r
+
+    mat = bwd()
+    with recomputing():
+        rec = bwd()
+    for nm, a, b in zip(("dQ", "dK", "dV"), mat[:3], rec[:3]):
+        assert torch.isfinite(a).all(), nm
+        assert _rel(a, b) <= FORM_TOL, f"{nm}: {_rel(a, b):.3e}"
 
 
 @pytest.mark.parametrize("name", list(CASES))
