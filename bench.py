@@ -499,7 +499,7 @@ def main(argv=None):
         return pmc_child(args.pmc_child, args.copy_calib_mib)
     if args.gpus != 1:
         print(f"bench.py: this engine is a single-GPU build; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "(multi-GPU sharding is design only in this build)", file=sys.stderr)
         return 2
 
     head = "d512_causal_gqa8_n16k"
@@ -580,7 +580,7 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(h["tflops_fwd_bwd"] / H100_FWDBWD_TFLOPS, 3),
-        "baseline_note": "vs reference H100 fp16 fwd+bwd 117.1 TFLOPS at this shape (BASELINE.md)",
+        "baseline_note": "vs the reference's published H100 fp16 fwd+bwd 117.1 TFLOPS at this shape",
         "dtype": "bf16",
         "data": "synthetic N(0,1), seed 0",
         "config": {"workload": head + "_fwd_bwd", "B": w["B"], "Hq": w["Hq"], "Hkv": w["Hkv"], "N": w["N"],
