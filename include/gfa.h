@@ -184,7 +184,8 @@ int gfa_bwd(const gfa_bwd_args* args);
  * q_splits = 0 takes the registry's split count, halved until its partials fit (1 needs none).
  * Every call on one GPU shares that GPU's scratch and leaves its contents there (a later
  * stages = GFA_BWD_DKV call reads the delta of the last GFA_BWD_DQ call): calls that overlap
- * on one GPU (concurrent streams or threads) race. Otherwise as gfa_bwd. */
+ * on one GPU (concurrent streams or threads) race. It always runs the recomputing form (a dS
+ * store does not fit a fixed scratch). Otherwise as gfa_bwd. */
 int gfa_bwd_noalloc(const gfa_bwd_args* args);
 
 /* Workspace bytes gfa_bwd needs for the given problem and q_splits (0 = registry choice) in the
