@@ -189,11 +189,9 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
     if (in0 || in1) {
       i16x8 b0[2], b1[2];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+      for (int ks = 0; ks < 2; ++ks) {  // (a block outside a unit's row is zeros in LDS)
         b0[ks] = tr_frag(st + u0 * DSB, soffA, soffB, ks * 256);
         b1[ks] = tr_frag(st + (u0 + 1) * DSB, soffA, soffB, ks * 256);
-        if (!in0) b0[ks] = i16x8{};
-        if (!in1) b1[ks] = i16x8{};
       }
       // Own scheduling region for the products: a fixed read-ahead of PF A fragments, two
       // transposing reads after each pair of products.
