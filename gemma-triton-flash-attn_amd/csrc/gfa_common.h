@@ -298,7 +298,10 @@ __device__ __forceinline__ void copy_rows_lds(const uint16_t* base, int64_t row_
 
 // The reverse of copy_rows_lds: one wave writes rows [row0, row0 + 32) of a (batch, head)
 // slice from an LDS block in the same layout, skipping rows at or past n_rows; each store
-// instruction covers whole rows (16 bytes per lane).
+// instruction covers whole rows (16 bytes per lane). The stores are non-temporal: an output row
+// is written once and not read by this kernel, and kept out of L2 it does not evict the tiles
+// that neighbouring workgroups are still reading (sliding-window forward 5% faster at C3, the
+// windowed dK/dV 1.5%; even elsewhere).
 template <int D>
 __device__ __forceinline__ void store_rows_lds(uint16_t* base, int64_t row_stride, int n_rows, int row0, int lane,
                                                const char GFA_LDS* blk) {
@@ -310,7 +313,8 @@ __device__ __forceinline__ void store_rows_lds(uint16_t* base, int64_t row_strid
   for (int i = 0; i < 32 / RPI; ++i) {
     const int r = i * RPI + lrow;
     const i16x8 v = lds_read16(blk, i * 1024 + lrow * (2 * D) + ((lc ^ swz<D>(r)) << 4));
-    if (row0 + r < n_rows) *reinterpret_cast<i16x8*>(base + (int64_t)(row0 + r) * row_stride + 8 * lc) = v;
+    if (row0 + r < n_rows)
+      __builtin_nontemporal_store(v, reinterpret_cast<i16x8*>(base + (int64_t)(row0 + r) * row_stride + 8 * lc));
   }
 }
 
