@@ -160,10 +160,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     // This role's rows (K or V) into tile buffer `wave` (idle before the loop) in whole-row
     // copies, read back in the operand layout.
     char GFA_LDS* blk = smem + wave * TILE;
-    if (role == 0) {
-      copy_rows_lds<D>(p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh, p.kv.sn, p.N, k0, lane, blk);
+    const uint16_t* src = role == 0 ? p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh
+                                    : p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh;
+    const int64_t sn = role == 0 ? p.kv.sn : p.vv.sn;
+    if (p.q_splits == 1) {  // no other workgroup reads these rows: non-temporal (C3 dK/dV 1.4%)
+      copy_rows_lds<D, true>(src, sn, p.N, k0, lane, blk);
     } else {
-      copy_rows_lds<D>(p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh, p.vv.sn, p.N, k0, lane, blk);
+      copy_rows_lds<D, false>(src, sn, p.N, k0, lane, blk);
     }
     drain_tile_copies();
 #pragma unroll
@@ -175,8 +178,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void bwd_dkv_kernel(const BwdDkvParam
     static_assert(NS == 2 && NU == 4, "one wave per 32 keys, four per workgroup");
     char GFA_LDS* kblk = smem + wave * TILE;
     char GFA_LDS* vblk = (char GFA_LDS*)stage_raw + wave * TILE;
-    copy_rows_lds<D>(p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh, p.kv.sn, p.N, k0, lane, kblk);
-    copy_rows_lds<D>(p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh, p.vv.sn, p.N, k0, lane, vblk);
+    if (p.q_splits == 1) {  // no other workgroup reads these rows: non-temporal
+      copy_rows_lds<D, true>(p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh, p.kv.sn, p.N, k0, lane, kblk);
+      copy_rows_lds<D, true>(p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh, p.vv.sn, p.N, k0, lane, vblk);
+    } else {
+      copy_rows_lds<D, false>(p.k + (int64_t)b * p.kv.sb + (int64_t)kvh * p.kv.sh, p.kv.sn, p.N, k0, lane, kblk);
+      copy_rows_lds<D, false>(p.v + (int64_t)b * p.vv.sb + (int64_t)kvh * p.vv.sh, p.vv.sn, p.N, k0, lane, vblk);
+    }
     drain_tile_copies();
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) {

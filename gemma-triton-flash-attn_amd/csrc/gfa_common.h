@@ -278,8 +278,9 @@ struct TileLoader {
 // n_rows repeating row n_rows - 1. Each of the D/16 direct global->LDS copies covers whole
 // rows (1 KB, coalesced); loading the same rows straight into the MFMA operand layout (lane =
 // row) touches 32 rows per instruction and is several times slower. The caller waits for
-// vmcnt before reading the block.
-template <int D>
+// vmcnt before reading the block. NT: non-temporal reads, for rows no other workgroup reads
+// (kept out of L2 they leave it to the shared tiles).
+template <int D, bool NT = false>
 __device__ __forceinline__ void copy_rows_lds(const uint16_t* base, int64_t row_stride, int n_rows, int row0, int lane,
                                               char GFA_LDS* blk) {
   constexpr int CPR = D / 8;
@@ -292,7 +293,7 @@ __device__ __forceinline__ void copy_rows_lds(const uint16_t* base, int64_t row_
   for (int i = 0; i < 32 / RPI; ++i) {
     const int r = i * RPI + lrow;
     const unsigned vo = (unsigned)min(row0 + r, n_rows - 1) * sb + (unsigned)((lc ^ swz<D>(r)) << 4);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void GFA_LDS*)(blk + i * 1024), 16, vo, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void GFA_LDS*)(blk + i * 1024), 16, vo, 0, 0, NT ? 2 : 0);
   }
 }
 
