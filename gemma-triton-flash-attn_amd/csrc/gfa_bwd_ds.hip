@@ -342,28 +342,58 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
   }
   drain_tile_copies();
 
-  // Column l32 of the accumulators is query sigma(l32) of the unit's tile; rows are head-dim
-  // elements DH dh + 32 db + 8 g + 4 h + 0..3.
-  const int c8 = l32 >> 3, e8 = l32 & 7;
+  // Epilogue. Column l32 of the accumulators is query sigma(l32) of the unit's tile, at row
+  // qoff of it; rows are head-dim elements DH dh + 32 db + 8 g + 4 h + 0..3. Each wave stages its
+  // half-rows (its two units x 32 queries x DH, scaled and rounded) through its own LDS block and
+  // stores them as whole half-rows, 16 bytes per lane and non-temporally (written once; 8-byte
+  // stores straight from the accumulators leave partial lines, which cannot go non-temporal).
+  // The staging blocks are the tile buffers: every wave must be past the loop first.
+  barrier_lds();
+  constexpr int HB = 32 * DH * 2;  // one unit's staged half-rows
+  constexpr int NCH = DH / 8;      // 16-byte chunks per half-row
+  static_assert(2 * HB <= TILE, "a tile buffer holds a wave's two staged units");
+  char GFA_LDS* stg0;
+  char GFA_LDS* stg1;
+  if constexpr (PAIRED) {
+    stg0 = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? K2 : K3;
+    stg1 = stg0 + HB;
+  } else {  // three tile buffers; the fourth wave's units go to two dS buffers (NW * DSB >= HB)
+    static_assert(NW * DSB >= HB, "a dS buffer holds one staged unit");
+    stg0 = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? K2 : S0;
+    stg1 = wave == 3 ? S1 : stg0 + HB;
+  }
+  const int ln = opaque(lane);
+  const int c8 = (ln & 31) >> 3, e8 = ln & 7;
   const int qoff = 16 * (c8 >> 1) + 8 * (e8 >> 2) + 4 * (c8 & 1) + (e8 & 3);
-  auto store = [&](int u, const f32x16 (&acc)[DBH]) __attribute__((always_inline)) {
-    const int q = qt_of(u) * 32 + qoff;
-    if (q < p.N) {
-      uint16_t* dqrow = p.dq + (int64_t)b * p.dqv.sb + (int64_t)head_of(u) * p.dqv.sh + (int64_t)q * p.dqv.sn + dh * DH;
+  auto stage = [&](const f32x16 (&acc)[DBH], char GFA_LDS* blk) __attribute__((always_inline)) {
 #pragma unroll
-      for (int db = 0; db < DBH; ++db) {
+    for (int db = 0; db < DBH; ++db) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          i16x4 o4;
+      for (int g = 0; g < 4; ++g) {
+        i16x4 o4;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[db][4 * g + e] * p.scale);
-          *reinterpret_cast<i16x4*>(dqrow + db * 32 + 8 * g + 4 * h) = o4;
-        }
+        for (int e = 0; e < 4; ++e) o4[e] = to16<IS_BF16>(acc[db][4 * g + e] * p.scale);
+        const int c = 4 * db + g;  // chunk of the half-row: elements 32 db + 8 g .. + 7
+        *reinterpret_cast<i16x4 GFA_LDS*>(blk + qoff * (DH * 2) + ((c ^ (qoff % NCH)) << 4) + 8 * (ln >> 5)) = o4;
       }
     }
   };
-  store(u0, acc0);
-  store(u0 + 1, acc1);
+  stage(acc0, stg0);
+  stage(acc1, stg1);
+  constexpr int RPI = 64 / NCH;  // half-rows per store instruction
+  auto put = [&](int u, const char GFA_LDS* blk) __attribute__((always_inline)) {
+    const int q0 = qt_of(u) * 32;
+    uint16_t* base = p.dq + (int64_t)b * p.dqv.sb + (int64_t)head_of(u) * p.dqv.sh + dh * DH;
+    const int c = ln % NCH;
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int r = i * RPI + ln / NCH;
+      const i16x8 v = lds_read16(blk, r * (DH * 2) + ((c ^ (r % NCH)) << 4));
+      if (q0 + r < p.N) __builtin_nontemporal_store(v, reinterpret_cast<i16x8*>(base + (int64_t)(q0 + r) * p.dqv.sn + 8 * c));
+    }
+  };
+  put(u0, stg0);
+  put(u0 + 1, stg1);
 }
 
 #define GFA_DS_INST(DD, WW)                                                                   \
