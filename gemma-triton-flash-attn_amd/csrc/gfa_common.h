@@ -264,7 +264,9 @@ struct TileLoader {
   __device__ __forceinline__ void load_part(int i, int row0, char GFA_LDS* tile) const {
     const int grp = i * NW + wave;
     const unsigned soff = (unsigned)(row0 + grp * RPI) * stride_b;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void GFA_LDS*)(tile + grp * 1024), 16, voff[i % NV], soff, 0, 0);
+    // sc0: each CU reads a tile once, into LDS, so the copy gains nothing from the CU's L1 (the
+    // workgroups that share a tile share it in L2); headline dK/dV 0.6% faster, the rest even.
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void GFA_LDS*)(tile + grp * 1024), 16, voff[i % NV], soff, 0, 1);
   }
 
   __device__ __forceinline__ void load(int row0, char GFA_LDS* tile) const {
