@@ -17,8 +17,8 @@ namespace gfa {
 // One workgroup per 32 rows of one (batch, head): each row's 16-byte chunks spread over the
 // lanes of one wave (whole rows per instruction, coalesced), partial products summed across
 // those lanes. Rows past N repeat row N - 1, as the recomputing dQ kernel writes them. O and dO
-// are read non-temporally (once each; kept out of L2 they leave it to the dK/dV kernel's tiles:
-// that stage 0.7% faster at the headline).
+// are read non-temporally (once each): 0.155 ms at the headline, 6.96 TB/s (0.183 ms before), and
+// kept out of L2 they leave it to the dK/dV kernel's tiles.
 template <int D, bool IS_BF16>
 __global__ __launch_bounds__(256) void delta_kernel(const DeltaParams p) {
   constexpr int CPR = D / 8;     // 16-byte chunks per row
