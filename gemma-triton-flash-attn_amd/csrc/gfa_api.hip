@@ -425,10 +425,11 @@ size_t ds_store_bytes(const gfa_bwd_args* a) {
   // the store's rows would be written; soft-capping and dropout are in the stored dS already.
   if (limit <= 0 || a->seg_lo != nullptr) return 0;
   const bool win = is_windowed(a->causal, a->window, a->seq_len);
-  if (!(a->head_dim == 512 || (a->head_dim == 256 && win))) return 0;
+  if (a->head_dim != 512 && a->head_dim != 256) return 0;  // below, the store's bytes outweigh the work saved
   const Entry* e = lookup(a->head_dim);
-  const DkvForm& f = bwd_dkv_form(e, a);  // the storing forms: the role pairs of 4 waves
-  if (f.roles != 2 || f.waves != 4 || f.bq != 32) return 0;
+  // The storing forms: 4 waves, 32-row query tiles (role pairs, or one wave per 32 keys at D=256).
+  const DkvForm& f = bwd_dkv_form(e, a);
+  if (f.waves != 4 || f.bq != 32 || (f.roles != 1 && f.roles != 2)) return 0;
   const gfa::DsLayout l = gfa::ds_layout(a->seq_len, a->causal, win ? a->window : 0);
   const size_t bytes = (size_t)a->batch * a->heads_q * (size_t)l.slab * 2048;
   return bytes <= (size_t)limit ? bytes : 0;

@@ -15,6 +15,8 @@
 // Which blocks exist is the dK/dV kernel's iteration: its workgroup w (keys 64 w .. 64 w + 63,
 // units 2 w and 2 w + 1) visits query tiles [2 w, nq) under causal masking, ending at
 // (64 w + 63 + window - 1) / 32 + 1 with a sliding window, and all tiles without causal masking.
+// The one-wave form's 128-key workgroups visit a superset of these (the tiles of their 64-key
+// halves) and store only the blocks inside jmin(i) .. jmax(i).
 // Per (batch, head) the blocks are stored query tile by query tile, each row of blocks holding
 // units jmin(i) .. jmax(i):
 // - no causal masking: all nk units, row stride nk;
@@ -51,6 +53,24 @@ __host__ __device__ inline int64_t ds_index(const DsLayout& l, int i, int j) {
   if (l.mode == 2) return (int64_t)i * l.lmax + (j - ds_jmin(l, i));
   const int64_t m = i >> 1;
   return 2 * m * m + 2 * m + (i & 1) * (2 * m + 2) + j;
+}
+
+// Query tiles [*lo, *hi) whose rows of blocks hold key unit j (jmin(i) <= j <= jmax(i)): those the
+// 64-key workgroup of unit j visits (from its first tile 2 (j >> 1) under causal masking, to the
+// end of its window).
+__host__ __device__ inline void ds_unit_rows(const DsLayout& l, int j, int* lo, int* hi) {
+  if (l.mode == 0) {
+    *lo = 0;
+    *hi = l.nq;
+    return;
+  }
+  const int m = j >> 1;
+  *lo = 2 * m;
+  *hi = l.nq;
+  if (l.mode == 2) {
+    const int e = (64 * m + 62 + l.window) / 32 + 1;
+    if (e < *hi) *hi = e;
+  }
 }
 
 // Host: the layout of an N-row problem (without the pointer) and its size in blocks per slab.

@@ -26,6 +26,11 @@ int main(int argc, char** argv) {
     for (int j = gfa::ds_jmin(l, i); j <= gfa::ds_jmax(l, i); ++j) printf(" %lld", (long long)gfa::ds_index(l, i, j));
     printf("\n");
   }
+  for (int j = 0; j < l.nk; ++j) {
+    int lo, hi;
+    gfa::ds_unit_rows(l, j, &lo, &hi);
+    printf("%d %d\n", lo, hi);
+  }
   return 0;
 }
 """
@@ -50,18 +55,20 @@ def layout_prog(tmp_path_factory):
     return str(exe)
 
 
-def dkv_visits(N, causal, window):
-    """(query tile, key unit) pairs the dK/dV kernel computes, per its workgroup loop."""
+def dkv_visits(N, causal, window, units=2):
+    """(query tile, key unit) pairs the dK/dV kernel computes, per its workgroup loop: workgroups
+    of `units` 32-key units (2: the role-pair forms, 4: the one-wave form)."""
     nq = (N + 31) // 32
     swa = causal and 0 < window < N
+    span = 32 * units
     out = set()
-    for kb in range((N + 63) // 64):
-        k0 = 64 * kb
-        k_last = min(N, k0 + 64) - 1
+    for kb in range((N + span - 1) // span):
+        k0 = span * kb
+        k_last = min(N, k0 + span) - 1
         lo = k0 // 32 if causal else 0
         hi = min(nq, (k_last + window - 1) // 32 + 1) if swa else nq
-        for u in (0, 1):
-            j = 2 * kb + u
+        for u in range(units):
+            j = units * kb + u
             if 32 * j >= N:
                 continue
             out.update((i, j) for i in range(lo, hi))
@@ -76,7 +83,8 @@ def test_store_matches_the_dkv_iteration(layout_prog, N, causal, window):
     nq, nk, lmax, slab = (int(x) for x in lines[0].split())
     assert nq == nk == (N + 31) // 32
     stored = {}
-    for i, line in enumerate(lines[1:]):
+    unit_rows = [tuple(int(x) for x in line.split()) for line in lines[1 + nq:]]
+    for i, line in enumerate(lines[1:1 + nq]):
         vals = [int(x) for x in line.split()]
         jmin, jmax, idx = vals[0], vals[1], vals[2:]
         assert 0 <= jmin <= jmax < nk, (i, jmin, jmax)
@@ -88,9 +96,19 @@ def test_store_matches_the_dkv_iteration(layout_prog, N, causal, window):
     visits = dkv_visits(N, causal, w)
     # dQ reads exactly the stored blocks; each must be written, and every write must land in one.
     assert set(stored) == visits
+    # The one-wave form (128-key workgroups) visits every stored block and stores the visited
+    # blocks inside jmin(i) .. jmax(i): exactly the layout again.
+    one_wave = dkv_visits(N, causal, w, units=4)
+    assert set(stored) <= one_wave
+    assert {(i, j) for (i, j) in one_wave if i < nq and stored.get((i, j)) is not None} == set(stored)
+    # ds_unit_rows (the one-wave form's test of which visited blocks to store): the query tiles
+    # holding unit j form the interval it returns
+    assert len(unit_rows) == nk
+    for j, (lo, hi) in enumerate(unit_rows):
+        assert {i for (i, jj) in stored if jj == j} == set(range(lo, hi)), (j, lo, hi)
     if w:
         assert lmax == max(jmax - jmin + 1 for jmin, jmax in
-                           ((int(l.split()[0]), int(l.split()[1])) for l in lines[1:]))
+                           ((int(l.split()[0]), int(l.split()[1])) for l in lines[1:1 + nq]))
 
 
 def test_workspace_sizes_and_forms():
@@ -105,20 +123,24 @@ def test_workspace_sizes_and_forms():
     base = _lib.bwd_workspace_size(1, 32, 4, 16384, 512, True, 0)
     nbytes, mat = backward_workspace(1, 32, 4, 16384, 512, True, 0)
     assert mat and nbytes == (base + 255) // 256 * 256 + 32 * 131584 * 2048
-    assert backward_workspace(1, 16, 8, 16384, 256, True, 1024)[1]          # windowed D=256
+    assert backward_workspace(1, 16, 8, 16384, 256, True, 1024)[1]          # windowed D=256 (role pairs)
     assert backward_workspace(2, 8, 2, 700, 512, False, 0, torch.float16)[1]  # non-causal D=512
-    for args in ((1, 16, 8, 16384, 256, True, 0), (1, 16, 8, 4096, 256, False, 0),  # D=256 without a window
-                 (1, 16, 2, 4096, 128, True, 1024), (1, 8, 8, 1024, 64, True, 0)):  # D=128, D=64
+    for args in ((1, 16, 8, 16384, 256, True, 0), (1, 16, 8, 4096, 256, False, 0),  # D=256 one-wave form
+                 (1, 16, 8, 4096, 256, True, 4096)):  # window >= N: full causal
+        assert backward_workspace(*args)[1], args
+    nb, m = backward_workspace(1, 16, 8, 4096, 256, True, 0)  # full causal: 8320 blocks per head (tiles i < 128: 2 (i >> 1) + 2)
+    assert m and nb == (_lib.bwd_workspace_size(1, 16, 8, 4096, 256, True, 0) + 255) // 256 * 256 + 16 * 8320 * 2048
+    for args in ((1, 16, 2, 4096, 128, True, 1024), (1, 8, 8, 1024, 64, True, 0)):  # D=128, D=64
         assert not backward_workspace(*args)[1], args
-    assert not backward_workspace(1, 16, 8, 4096, 256, True, 4096)[1]  # window >= N: full causal D=256
     nb, m = backward_workspace(1, 8, 1, 2048, 512, True, 0, segments=True)  # segment tables: recomputing
     assert not m and nb == _lib.bwd_workspace_size(1, 8, 1, 2048, 512, True, 0)
     for kw in ({"softcap": 30.0}, {"dropout_p": 0.1}):
         assert backward_workspace(1, 8, 1, 2048, 512, True, 0, **kw)[1], kw  # in the stored dS
         assert backward_workspace(1, 8, 1, 2048, 512, True, 500, **kw)[1], kw
-        # windowed D=256: their instances are the one-wave dK/dV form, which stores nothing
-        nb, m = backward_workspace(1, 16, 8, 4096, 256, True, 1024, **kw)
-        assert not m and nb == _lib.bwd_workspace_size(1, 16, 8, 4096, 256, True, 1024), kw
+        # D=256: their instances are the one-wave dK/dV form, which stores too
+        assert backward_workspace(1, 16, 8, 4096, 256, True, 1024, **kw)[1], kw
+        assert backward_workspace(1, 16, 8, 4096, 256, False, 0, **kw)[1], kw
+        assert not backward_workspace(1, 16, 8, 4096, 128, True, 0, **kw)[1], kw
     prev = _lib.set_bwd_ds_limit(0)
     try:
         assert _lib.bwd_ds_limit() == 0

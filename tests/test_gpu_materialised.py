@@ -31,6 +31,14 @@ CASES = {
     "d256_swa700_ragged": (1, 16, 4, 3000, 256, True, 700, torch.bfloat16, 0),
     "d256_swa31": (2, 8, 2, 517, 256, True, 31, torch.bfloat16, 0),
     "d256_swa512_fp16": (1, 8, 1, 1500, 256, True, 512, torch.float16, 0),
+    # D=256 without a window: the one-wave dK/dV form (128-key workgroups) stores
+    "d256_causal_gqa2": (1, 16, 8, 2048, 256, True, 0, torch.bfloat16, 0),
+    "d256_causal_ragged": (1, 8, 2, 3001, 256, True, 0, torch.bfloat16, 0),
+    "d256_noncausal_b2": (2, 8, 2, 700, 256, False, 0, torch.bfloat16, 0),
+    "d256_causal_fp16": (1, 8, 1, 1100, 256, True, 0, torch.float16, 0),
+    "d256_qsplit4": (1, 8, 1, 2048, 256, True, 0, torch.bfloat16, 4),
+    "d256_tiny": (1, 4, 1, 33, 256, True, 0, torch.bfloat16, 0),
+    "d256_window_ge_n": (1, 8, 2, 1000, 256, True, 1000, torch.bfloat16, 0),
 }
 
 
@@ -54,14 +62,18 @@ FEATURE_CASES = {
     "d512_dropout": (1, 8, 2, 1024, 512, True, 0, torch.bfloat16, 0.0, 0.1),
     "d512_swa700_softcap50_fp16": (1, 8, 2, 3000, 512, True, 700, torch.float16, 50.0, 0.0),
     "d512_swa512_dropout_b2": (2, 4, 1, 1500, 512, True, 512, torch.bfloat16, 0.0, 0.15),
+    "d256_softcap30": (1, 8, 2, 1500, 256, True, 0, torch.bfloat16, 30.0, 0.0),
+    "d256_swa700_softcap50_fp16": (1, 8, 2, 3000, 256, True, 700, torch.float16, 50.0, 0.0),
+    "d256_noncausal_dropout": (2, 4, 1, 900, 256, False, 0, torch.bfloat16, 0.0, 0.1),
+    "d256_swa100_dropout": (1, 8, 4, 1300, 256, True, 100, torch.bfloat16, 0.0, 0.15),
 }
 
 
 @pytest.mark.parametrize("name", list(FEATURE_CASES))
 def test_materialised_softcap_dropout(name, device):
-    """Soft-capping and dropout take the materialised form too at D=512 (the dK/dV kernel's
-    stored dS carries the soft-cap factor 1 - t^2 and the dropped dP); against the recomputing
-    form. (At D=256 their dK/dV instances are the one-wave form, which stores nothing: recomputing.)"""
+    """Soft-capping and dropout take the materialised form too (the dK/dV kernel's stored dS
+    carries the soft-cap factor 1 - t^2 and the dropped dP; at D=256 their dK/dV instances are
+    the one-wave form, with or without a window); against the recomputing form."""
     from gemma_triton_flash_attn_amd.attention import _backward, _forward, backward_workspace
 
     B, Hq, Hkv, N, D, causal, window, dtype, cap, dp = FEATURE_CASES[name]
