@@ -223,9 +223,10 @@ def bench_workload(name, w, steps, warmup, device, kernels=True, layout="bhnd", 
 
 # Kernel-name tags per timed stage: the dQ stage is bwd_dq_kernel in the recomputing backward and
 # bwd_dq_ds_kernel in the materialised one, whose dK/dV stage runs delta_kernel, then bwd_dkv_kernel
-# (a stage's traffic is the sum over its kernels, as its time is).
+# (bwd_dkv_ds_kernel for the one-wave D=256 form); a stage's traffic is the sum over its kernels,
+# as its time is.
 KERNEL_TAGS = {"fwd": ("fwd_kernel",), "dq": ("bwd_dq_kernel", "bwd_dq_ds_kernel"),
-               "dkv": ("bwd_dkv_kernel", "delta_kernel")}
+               "dkv": ("bwd_dkv_kernel", "bwd_dkv_ds_kernel", "delta_kernel")}
 PMC_COUNTERS = ("FETCH_SIZE", "WRITE_SIZE")  # KiB per dispatch, one counter per rocprofv3 pass
 
 
