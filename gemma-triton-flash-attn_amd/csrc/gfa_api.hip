@@ -421,9 +421,9 @@ namespace {
 std::atomic<int64_t> g_ds_limit{int64_t(32) << 30};
 size_t ds_store_bytes(const gfa_bwd_args* a) {
   const int64_t limit = g_ds_limit.load();
-  // Segment tables trim the dK/dV kernel's query-tile ranges per key block, so not every block of
-  // the store's rows would be written; soft-capping and dropout are in the stored dS already.
-  if (limit <= 0 || a->seg_lo != nullptr) return 0;
+  // Segment tables trim the dK/dV kernel's query-tile ranges per key block and the dQ kernel
+  // reads the same blocks (ds_seg_units); soft-capping and dropout are in the stored dS already.
+  if (limit <= 0) return 0;
   const bool win = is_windowed(a->causal, a->window, a->seq_len);
   if (a->head_dim != 512 && a->head_dim != 256) return 0;  // below, the store's bytes outweigh the work saved
   const Entry* e = lookup(a->head_dim);
@@ -591,6 +591,8 @@ int bwd_impl(const gfa_bwd_args* a, float* delta_buf, void* ws_buf, size_t ws_by
     }
     if (stages & GFA_BWD_DQ) {
       gfa::BwdDqDsParams pz;
+      pz.seg_lo = a->seg_lo;
+      pz.seg_hi = a->seg_hi;
       pz.k = pq.k;
       pz.dq = pq.dq;
       pz.kv = pq.kv;

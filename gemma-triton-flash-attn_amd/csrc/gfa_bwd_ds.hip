@@ -106,18 +106,42 @@ __global__ __launch_bounds__(256, WPE) void bwd_dq_ds_kernel(const BwdDqDsParams
   const int qsb = p.dsl.mode == 1 ? (p.g.n_qsb - 1 - lid) : lid;
   auto head_of = [&](int u) __attribute__((always_inline)) { return kvh * p.R + hg * p.g.hpw + u % p.g.hpw; };
   auto qt_of = [&](int u) __attribute__((always_inline)) { return qsb * p.g.qbw + u / p.g.hpw; };
-  // unit u's row of blocks [jlo, jhi] (empty past the last query tile)
-  auto jlo_of = [&](int u) __attribute__((always_inline)) { return qt_of(u) < p.dsl.nq ? ds_jmin(p.dsl, qt_of(u)) : 1; };
-  auto jhi_of = [&](int u) __attribute__((always_inline)) { return qt_of(u) < p.dsl.nq ? ds_jmax(p.dsl, qt_of(u)) : 0; };
+  // Query tile qt's stored blocks [jlo, jhi]: the layout's row, narrowed by the segment table to
+  // the blocks the dK/dV kernel computes there (empty past the last query tile).
+  const int* slo = p.seg_lo ? p.seg_lo + (int64_t)b * p.N : nullptr;
+  const int* shi = p.seg_lo ? p.seg_hi + (int64_t)b * p.N : nullptr;
+  auto jlo_at = [&](int qt) __attribute__((always_inline)) {
+    if (qt >= p.dsl.nq) return 1;
+    int lo = ds_jmin(p.dsl, qt);
+    if (slo) {
+      int a, c;
+      ds_seg_units(slo, shi, p.N, qt, &a, &c);
+      lo = max(lo, a);
+    }
+    return lo;
+  };
+  auto jhi_at = [&](int qt) __attribute__((always_inline)) {
+    if (qt >= p.dsl.nq) return 0;
+    int hi = ds_jmax(p.dsl, qt);
+    if (slo) {
+      int a, c;
+      ds_seg_units(slo, shi, p.N, qt, &a, &c);
+      hi = min(hi, c);
+    }
+    return hi;
+  };
+  auto jlo_of = [&](int u) __attribute__((always_inline)) { return jlo_at(qt_of(u)); };
+  auto jhi_of = [&](int u) __attribute__((always_inline)) { return jhi_at(qt_of(u)); };
 
-  // Tile range: the union of the workgroup's rows of blocks (jmin and jmax do not decrease
-  // with the query tile), made a multiple of the loop's unroll (four or three tiles).
+  // Tile range: the union of the workgroup's rows of blocks (both bounds do not decrease with
+  // the query tile), made a multiple of the loop's unroll (four or three tiles); empty when a
+  // segment table leaves the workgroup's tiles no block.
   constexpr int UNROLL = PAIRED ? 4 : 3;
   const int wg_qt_lo = qsb * p.g.qbw;
   const int wg_qt_last = min(p.dsl.nq, wg_qt_lo + p.g.qbw) - 1;
-  const int t_lo = ds_jmin(p.dsl, wg_qt_lo);
-  const int t_last = ds_jmax(p.dsl, wg_qt_last);
-  const int t_hi = t_lo + (t_last + 1 - t_lo + UNROLL - 1) / UNROLL * UNROLL;
+  const int t_lo = jlo_at(wg_qt_lo);
+  const int t_last = jhi_at(wg_qt_last);
+  const int t_hi = t_last >= t_lo ? t_lo + (t_last + 1 - t_lo + UNROLL - 1) / UNROLL * UNROLL : t_lo;
   const int jlo0 = jlo_of(u0), jhi0 = jhi_of(u0), jlo1 = jlo_of(u0 + 1), jhi1 = jhi_of(u0 + 1);
 
   TileLoader<D, BKV, NW> kload;

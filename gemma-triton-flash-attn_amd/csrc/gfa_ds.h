@@ -73,6 +73,30 @@ __host__ __device__ inline void ds_unit_rows(const DsLayout& l, int j, int* lo, 
   }
 }
 
+// Segment tables (each row a partition of [0, N) into runs: a segment's tokens carry lo = its
+// first token and hi = one past its last, a padding token t carries lo = hi = t): the key units
+// [*jlo, *jhi] whose blocks of query tile i the dK/dV kernel computes, before the layout's own
+// bounds. Its 64-key workgroup of keys g0 .. glast visits the tiles [lo[g0] / 32,
+// ceil(hi[glast] / 32)), so unit j is in for tile i (rows r0 = 32 i .. r1) when
+// - lo[g0] <= r0 + 31, i.e. g0 < max(r0 + 32, hi[r1]) (a key past the tile shares its segment
+//   with row r1 exactly when it lies before hi[r1]);
+// - hi[glast] > r0, i.e. glast >= lo[r0] (keys before r0 reach past it exactly when they share
+//   row r0's segment), except for glast = r0 itself when that row is padding.
+// Table values are clamped to [0, N], as the kernels clamp them. The one-wave form's 128-key
+// workgroups visit a superset (their first key is no later, their last no earlier).
+__host__ __device__ inline void ds_seg_units(const int* lo, const int* hi, int N, int i, int* jlo, int* jhi) {
+  auto cl = [N](int x) { return x < 0 ? 0 : (x > N ? N : x); };
+  const int r0 = 32 * i;
+  const int r1 = r0 + 31 < N - 1 ? r0 + 31 : N - 1;
+  int j0 = 2 * (cl(lo[r0]) / 64);  // the first unit whose workgroup's last key reaches lo[r0]
+  const int g_end = 64 * (j0 >> 1) + 64;
+  if (cl(hi[(g_end < N ? g_end : N) - 1]) <= r0) j0 += 2;
+  const int h1 = cl(hi[r1]);
+  const int e = h1 > r0 + 32 ? h1 : r0 + 32;
+  *jlo = j0;
+  *jhi = 2 * ((e - 1) / 64) + 1;
+}
+
 // Host: the layout of an N-row problem (without the pointer) and its size in blocks per slab.
 inline DsLayout ds_layout(int N, int causal, int window) {
   DsLayout l;

@@ -138,6 +138,8 @@ struct DeltaParams {
 
 // dQ = scale * dS K from the dS store (the materialised backward).
 struct BwdDqDsParams {
+  const int* seg_lo;  // optional (B, N) segment table (with seg_hi), or null
+  const int* seg_hi;
   const uint16_t* k;
   uint16_t* dq;
   RowView kv, dqv;

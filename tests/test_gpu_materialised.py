@@ -118,6 +118,62 @@ def test_materialised_matches_recomputing(name, device):
     assert float((mat[3][..., :N] - rec[3][..., :N]).abs().max()) <= 1e-3
 
 
+SEG_CASES = {
+    # name: B, Hq, Hkv, N, D, causal, window, dtype, table ("cu": cu_seqlens of one row, "len": the
+    # rows' lengths, "left": the same left-padded), extra features
+    "d512_packed": (1, 8, 2, 2000, 512, True, 0, torch.bfloat16, ("cu", [0, 300, 301, 1200, 1900]), {}),
+    "d512_noncausal_lengths_b2": (2, 8, 2, 1100, 512, False, 0, torch.bfloat16, ("len", [1063, 550]), {}),
+    "d512_left_padding_b2_fp16": (2, 4, 1, 900, 512, True, 0, torch.float16, ("left", [860, 897]), {}),
+    "d512_swa300_packed_softcap": (1, 8, 1, 1500, 512, True, 300, torch.bfloat16,
+                                   ("cu", [0, 700, 705, 1400]), {"softcap": 30.0}),
+    "d512_padding_row_alone": (1, 4, 1, 993, 512, True, 0, torch.bfloat16, ("cu", [0, 500, 992]), {}),
+    "d256_swa512_packed": (1, 16, 8, 3000, 256, True, 512, torch.bfloat16, ("cu", [0, 1000, 1001, 2500, 2999]), {}),
+    "d256_causal_packed_full": (1, 8, 2, 2048, 256, True, 0, torch.bfloat16, ("cu", [0, 64, 700, 1500, 2048]), {}),
+    "d256_noncausal_lengths_b2": (2, 8, 4, 777, 256, False, 0, torch.bfloat16, ("len", [777, 400]), {}),
+    "d256_padding_row_alone_dropout": (1, 4, 2, 993, 256, True, 0, torch.bfloat16, ("cu", [0, 500, 992]),
+                                       {"dropout_p": 0.1}),
+}
+
+
+@pytest.mark.parametrize("name", list(SEG_CASES))
+def test_materialised_with_segments(name, device):
+    """Segment tables (packed sequences, padding) in the materialised form: the dQ kernel reads
+    only the blocks the segment-trimmed dK/dV iteration writes (ds_seg_units). Against the
+    recomputing form; padding rows get dQ exactly 0 (their dS rows are 0)."""
+    import gemma_triton_flash_attn_amd as gfa
+    from gemma_triton_flash_attn_amd.attention import _backward, _forward, backward_workspace
+
+    B, Hq, Hkv, N, D, causal, window, dtype, (kind, spec), kw = SEG_CASES[name]
+    print(f"case {name}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal} window={window} {dtype} "
+          f"{kind}={spec} {kw}", flush=True)
+    if kind == "cu":
+        segs = gfa.segments.from_cu_seqlens(spec, N, device=device)
+    else:
+        segs = gfa.segments.from_lengths(spec, N, left_padding=kind == "left", device=device)
+    assert backward_workspace(B, Hq, Hkv, N, D, causal, window, dtype, segments=True, **kw)[1]
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, dtype, device, seed=N + 11)
+    sc = D ** -0.5
+    kw = dict(kw, dropout_seed=77) if kw.get("dropout_p") else kw
+    o, lse = _forward(q, k, v, causal, window, sc, store_lse=True, segments=segs, **kw)
+
+    def bwd():
+        r = _backward(q, k, v, o, lse, do, causal, window, sc, segments=segs, **kw)
+        torch.cuda.synchronize()
+        return r
+
+    mat = bwd()
+    with recomputing():
+        rec = bwd()
+    for nm, a, b in zip(("dQ", "dK", "dV"), mat[:3], rec[:3]):
+        assert torch.isfinite(a).all(), nm
+        assert _rel(a, b) <= FORM_TOL, f"{nm}: {_rel(a, b):.3e}"
+    lo, hi = segs
+    pad = (lo == hi).to(device)  # (B, N): padding tokens (none in a fully packed row)
+    if bool(pad.any()):
+        dq_pad = mat[0].float().permute(0, 2, 1, 3)[pad]  # (padding tokens, Hq, D)
+        assert float(dq_pad.abs().max()) == 0.0
+
+
 def test_stage_split_through_the_workspace_is_bitwise(device):
     """GFA_BWD_DKV (delta and dK/dV, storing dS), then GFA_BWD_DQ reading the store the first call
     left in the same workspace, equals the one-call backward bit for bit."""
