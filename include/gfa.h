@@ -165,8 +165,9 @@ int gfa_fwd(const gfa_fwd_args* args);
  *   it computes (16-bit, in the workspace), then dQ = scale * dS K from that store. It replaces
  *   two thirds of the dQ kernel's matrix work with 2 KiB of dS per block, written once and read
  *   once. Runs when the workspace holds the store (gfa_bwd_workspace_bytes), the store is within
- *   gfa_bwd_ds_limit, head_dim is 256 or 512 (soft-capping and dropout included: they are in
- *   the stored dS) and the problem has no segment table; otherwise the recomputing form runs. */
+ *   gfa_bwd_ds_limit and head_dim is 256 or 512 (soft-capping, dropout and segment tables
+ *   included: the first two are in the stored dS, and the dQ kernel reads only the blocks the
+ *   segment-trimmed dK/dV kernel writes); otherwise the recomputing form runs. */
 int gfa_bwd(const gfa_bwd_args* args);
 
 /* Bytes of the library-owned device scratch of gfa_bwd_noalloc, per GPU. */
