@@ -194,6 +194,30 @@ def test_stage_split_through_the_workspace_is_bitwise(device):
     assert torch.equal(bufs[3][..., :N], full[3][..., :N])
 
 
+def test_stage_split_with_segments_is_bitwise(device):
+    """The stage split with a segment table (both calls take it): GFA_BWD_DKV then GFA_BWD_DQ
+    through one workspace equals the one-call backward bit for bit."""
+    import gemma_triton_flash_attn_amd as gfa
+    from gemma_triton_flash_attn_amd import _lib
+    from gemma_triton_flash_attn_amd.attention import _backward, _forward, backward_workspace
+
+    B, Hq, Hkv, N, D = 1, 8, 2, 1300, 512
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, torch.bfloat16, device, seed=9)
+    segs = gfa.segments.from_cu_seqlens([0, 400, 401, 1250], N, device=device)
+    sc = D ** -0.5
+    o, lse = _forward(q, k, v, True, 0, sc, store_lse=True, segments=segs)
+    full = _backward(q, k, v, o, lse, do, True, 0, sc, segments=segs)
+    nbytes, mat = backward_workspace(B, Hq, Hkv, N, D, True, 0, segments=True)
+    assert mat
+    bufs = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(full[3]),
+            torch.empty(nbytes, dtype=torch.uint8, device=device))
+    _backward(q, k, v, o, lse, do, True, 0, sc, out=bufs, stages=_lib.GFA_BWD_DKV, segments=segs)
+    _backward(q, k, v, o, lse, do, True, 0, sc, out=bufs, stages=_lib.GFA_BWD_DQ, segments=segs)
+    torch.cuda.synchronize()
+    for nm, a, b in zip(("dQ", "dK", "dV"), bufs[:3], full[:3]):
+        assert torch.equal(a, b), nm
+
+
 def test_store_limit_selects_the_form(device):
     """A store above the limit runs the recomputing form (bit for bit the limit-0 results); the
     limit restored, the materialised one again."""
